@@ -1,0 +1,142 @@
+/*
+ * m5k.h -- C ABI of libm5k.so, the MI355X (gfx950) quantized-projection hot path.
+ *
+ * Every entry point takes device pointers to row-major, contiguous buffers,
+ * 64-bit sizes and an opaque HIP stream (hipStream_t passed as void*; NULL is
+ * the default stream). Launches are asynchronous on that stream. Inputs are
+ * never written. The library never allocates device memory: the caller owns
+ * every buffer, outputs included.
+ *
+ * Return value: 0 on success; a nonzero M5K_E* code otherwise, with a
+ * human-readable message available from m5k_last_error() on the calling
+ * thread. Argument checks here cover only what the kernels rely on for memory
+ * safety and launch validity; the Python layer reproduces the reference's
+ * ValueError / NotImplementedError contract before calling in.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   quantize                 src/m5kernels/metal.py:27-44
+ *   gemm                     src/m5kernels/metal.py:158-269
+ *   rotate                   src/m5kernels/hadamard.py:33-77
+ *   fused_norm_hadamard_quantize
+ *                            src/m5kernels/norm_hadamard.py:122-176
+ *   fused_gated_residual_norm_hadamard_quantize
+ *                            src/m5kernels/norm_hadamard.py:198-265
+ *   gated_residual_add       src/m5kernels/norm_hadamard.py:280-300
+ *   unfused_norm             src/m5kernels/norm_hadamard.py:321-348
+ *   projection_qk_rope       src/m5kernels/qk_rope.py:120-182
+ *   qk_norm_rope             src/m5kernels/qk_rope.py:185-203
+ */
+#ifndef M5K_H
+#define M5K_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+#define M5K_F32 0
+#define M5K_F16 1
+#define M5K_BF16 2
+#define M5K_I8 3
+#define M5K_U8 4
+#define M5K_I32 5
+
+/* Quantization modes. */
+#define M5K_QUANT_INT8 0 /* symmetric [-127,127], scale = peak/127 */
+#define M5K_QUANT_FP8 1  /* OCP E4M3 codes in uint8, scale = peak/448 */
+
+/* Normalization kinds for the fused prep. */
+#define M5K_NORM_RMS 0
+#define M5K_NORM_LAYER 1
+
+/* Status codes. */
+#define M5K_OK 0
+#define M5K_EINVAL 1  /* argument outside what the kernels support */
+#define M5K_ELAUNCH 2 /* HIP launch or runtime error */
+
+/* Message for the last failure on this thread ("" if none). */
+const char* m5k_last_error(void);
+
+/* ABI version (major*100 + minor). */
+int m5k_abi_version(void);
+
+/*
+ * Per-row symmetric quantizer.  Replaces metal.quantize(x, mode) for modes
+ * "int8" and "fp8" (src/m5kernels/metal.py:27-44, shaders/quantize.metal:1-38).
+ * x: [rows,k] of x_dtype (F32/F16/BF16).  q: [rows,k] int8 (INT8) or uint8
+ * E4M3 codes (FP8).  scales: [rows] float32.
+ * peak = max|x|; scale = peak==0 ? 1 : peak/127 (or /448), IEEE fp32 division;
+ * INT8 code = clamp(rint_even(x/scale), -127, 127); FP8 code = nearest E4M3
+ * (ties to even, saturating at 448, sign from the sign bit).
+ */
+int m5k_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int mode,
+                      void* q, float* scales, void* stream);
+
+/*
+ * W8A8 linear.  Replaces metal.gemm(a, b, "int8", ...) (src/m5kernels/metal.py:158-269,
+ * epilogues :88-128).  a: [m,k] int8, b: [n,k] int8 (weights, K-contiguous).
+ * c[m,n] = O(float(sum_k a*b) * a_scales[m] * b_scales[n] [+ bias]) with int32
+ * accumulation and the FP32 products evaluated left to right; O = c_dtype
+ * (F32/F16/BF16, round to nearest even).
+ * bias (optional, may be NULL): float32 [n], or [P,n] selected by
+ *   bias_row_map[m] (int32) when bias_row_map is non-NULL.
+ * residual/gate (optional, both or neither; excludes bias; c_dtype must be BF16):
+ *   residual bf16 [m,n], gate bf16 [n] or [P,n] with gate_row_map[m];
+ *   c = bf16(float(residual) + float(bf16(branch)) * float(gate)).
+ */
+int m5k_gemm_i8(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                const float* bias, const int32_t* bias_row_map,
+                const void* residual, const void* gate, const int32_t* gate_row_map,
+                void* stream);
+
+/*
+ * Raw INT32 accumulators of the W8A8 GEMM (test hook for bit-exact parity):
+ * acc[m,n] = sum_k a[m,k]*b[n,k].  Same kernel main loop as m5k_gemm_i8.
+ */
+int m5k_gemm_i8_acc(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                    int32_t* acc, void* stream);
+
+/*
+ * FP8 E4M3 linear with FP32 accumulation.  Replaces metal.gemm(a, b, "fp8", ...)
+ * (src/m5kernels/metal.py:75-80,191-194).  a: [m,k], b: [n,k] uint8 E4M3 codes;
+ * k % 128 == 0.  c = O(acc * a_scales[m] * b_scales[n]).
+ */
+int m5k_gemm_f8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                void* stream);
+
+/*
+ * Floating GEMM with FP32 accumulation.  Replaces metal.gemm(a, b, "bf16"|"fp16", ...)
+ * (src/m5kernels/metal.py:59-74,101-107).  a: [m,k], b: [n,k] of ab_dtype (BF16/F16).
+ * c = O(acc).  Optional gated residual epilogue as for m5k_gemm_i8 (BF16 only).
+ */
+int m5k_gemm_float(const void* a, const void* b, int ab_dtype, int64_t m, int64_t n, int64_t k,
+                   void* c, int c_dtype, const void* residual, const void* gate,
+                   const int32_t* gate_row_map, void* stream);
+
+/*
+ * Signed block-Hadamard rotation  Y = (X * signs) H_B, FP32 output.
+ * Replaces hadamard.rotate (src/m5kernels/hadamard.py:33-77, shaders/hadamard.metal:1-26).
+ * x: [rows,k] of x_dtype, signs: int8 [k] (+-1), block in {32,...,1024}, k % block == 0.
+ * Natural-order Sylvester butterflies in FP32, then one multiply by the FP32
+ * constant 1/sqrt(block).
+ */
+int m5k_hadamard_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int block,
+                        const int8_t* signs, float* y, void* stream);
+
+/*
+ * Fused rotation + per-row INT8 quantization: the codes and scales of
+ * quantize(rotate(x, block, signs), "int8") without materializing the FP32
+ * rotation (the online composition of src/m5kernels/hadamard_gemm.py:27-69).
+ */
+int m5k_hadamard_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int block,
+                               const int8_t* signs, int8_t* q, float* scales, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* M5K_H */

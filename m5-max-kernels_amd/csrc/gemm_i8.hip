@@ -1,0 +1,44 @@
+// C-ABI entry points of the W8A8 (INT8 x INT8 -> INT32) linear; kernels in gemm_launch.h.
+#include "gemm_launch.h"
+
+using namespace m5k;
+using namespace m5k::gemm;
+using namespace m5k::gemm::detail;
+
+extern "C" int m5k_gemm_i8(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                           const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                           const float* bias, const int32_t* bias_row_map, const void* residual,
+                           const void* gate, const int32_t* gate_row_map, void* stream) {
+  clear_error();
+  const char* name = "m5k_gemm_i8";
+  if (int rc = check_shape(m, n, k, name)) return rc;
+  M5K_REQUIRE(a && b && c && a_scales && b_scales, "%s: null operand, scale or output pointer", name);
+  M5K_REQUIRE(k <= 133144, "%s: K=%lld exceeds the INT32 worst-case bound 133144", name, (long long)k);
+  M5K_REQUIRE(!bias_row_map || bias, "%s: bias_row_map requires bias", name);
+  M5K_REQUIRE((residual == nullptr) == (gate == nullptr), "%s: residual and gate go together", name);
+  M5K_REQUIRE(!gate_row_map || gate, "%s: gate_row_map requires gate", name);
+  M5K_REQUIRE(!(bias && residual), "%s: bias and gated residual cannot be combined", name);
+  M5K_REQUIRE(!residual || c_dtype == M5K_BF16, "%s: gated epilogue requires BF16 output", name);
+  EpiParams p{a_scales, b_scales, c, bias, bias_row_map, static_cast<const uint16_t*>(residual),
+              static_cast<const uint16_t*>(gate), gate_row_map};
+  hipStream_t st = as_stream(stream);
+  switch (c_dtype) {
+    case M5K_BF16: return launch_i8<M5K_BF16>(a, b, m, n, k, p, st);
+    case M5K_F16: return launch_i8<M5K_F16>(a, b, m, n, k, p, st);
+    case M5K_F32: return launch_i8<M5K_F32>(a, b, m, n, k, p, st);
+    default: set_error("%s: unsupported output dtype %d", name, c_dtype); return M5K_EINVAL;
+  }
+}
+
+extern "C" int m5k_gemm_i8_acc(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                               int32_t* acc, void* stream) {
+  clear_error();
+  const char* name = "m5k_gemm_i8_acc";
+  if (int rc = check_shape(m, n, k, name)) return rc;
+  M5K_REQUIRE(a && b && acc, "%s: null pointer", name);
+  M5K_REQUIRE(k <= 133144, "%s: K exceeds the INT32 worst-case bound", name);
+  EpiParams p{};
+  p.c = acc;
+  return launch<I8, M5K_I32, EPI_NONE, EPI_NONE, true>(a, b, m, n, k, p, as_stream(stream), name);
+}
+

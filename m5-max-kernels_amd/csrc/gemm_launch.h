@@ -1,0 +1,119 @@
+// W8A8 / FP8 / BF16 / FP16 linear layers on gfx950 MFMA with fused epilogues.
+//
+// Contract: src/m5kernels/metal.py:158-269 (gemm) with the epilogue strings of
+// metal.py:88-128:
+//   quantized  C = O(float(acc) * AS[row] * BS[col])            (left to right, FP32)
+//   + bias     C = O(float(acc) * AS[row] * BS[col] + Bias[..])  (before the output cast)
+//   gated      branch = bf16(value); C = bf16(float(Residual) + float(branch) * float(Gate[..]))
+//   float      C = O(float(acc))
+// The library is compiled with -ffp-contract=off so none of these products and sums is
+// fused into an FMA: the FP32 rounding sequence is exactly the one written above.
+#pragma once
+#include "gemm_core.h"
+
+namespace m5k {
+namespace gemm {
+namespace detail {
+
+enum { EPI_NONE = 0, EPI_VECTOR = 1, EPI_TABLE = 2 };
+
+struct EpiParams {
+  const float* sa;
+  const float* sb;
+  void* c;
+  const float* bias;
+  const int32_t* bias_map;
+  const uint16_t* residual;
+  const uint16_t* gate;
+  const int32_t* gate_map;
+};
+
+// RAW: write INT32 accumulators (I8 only).
+template <int MODE, bool ALIGNED, int OUT_DT, int BIAS, int GATE, bool RAW>
+__global__ __launch_bounds__(THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
+                                                          const uint8_t* __restrict__ B, int M, int N,
+                                                          int64_t Kb, EpiParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * STAGE_BYTES];
+  using acc_t = typename Traits<MODE>::acc_t;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  acc_t acc[FM][FN];
+  mainloop<MODE, ALIGNED>(A, B, M, N, Kb, m0, n0, smem, acc);
+
+  for_each_acc(acc, m0, n0, [&](int m, int n, auto v) {
+    if (m >= M || n >= N) return;
+    const int64_t idx = (int64_t)m * N + n;
+    if constexpr (RAW) {
+      static_cast<int32_t*>(p.c)[idx] = v;
+    } else {
+      float value;
+      if constexpr (MODE == I8 || MODE == F8) value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
+      else value = v;
+      if constexpr (BIAS != EPI_NONE) {
+        const int64_t boff = BIAS == EPI_TABLE ? (int64_t)p.bias_map[m] * N : 0;
+        value = value + p.bias[boff + n];
+      }
+      if constexpr (GATE != EPI_NONE) {
+        const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;
+        const float branch = round_through<M5K_BF16>(value);
+        const float res = bf16_bits_to_f32(p.residual[idx]);
+        const float g = bf16_bits_to_f32(p.gate[goff + n]);
+        store_elem<M5K_BF16>(p.c, idx, res + branch * g);
+      } else {
+        store_elem<OUT_DT>(p.c, idx, value);
+      }
+    }
+  });
+}
+
+template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
+int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
+           hipStream_t st, const char* name) {
+  const int64_t kb = k * Traits<MODE>::elem_bytes;
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  M5K_REQUIRE(tiles <= 0x7FFFFFFF, "%s: too many tiles", name);
+  const bool aligned = kb % 16 == 0 && aligned16(a) && aligned16(b);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(THREADS);
+  auto* A = static_cast<const uint8_t*>(a);
+  auto* B = static_cast<const uint8_t*>(b);
+  if (aligned)
+    gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, p);
+  else
+    gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, p);
+  return launch_status(name);
+}
+
+inline int check_shape(int64_t m, int64_t n, int64_t k, const char* name) {
+  M5K_REQUIRE(m > 0 && n > 0 && k > 0, "%s: empty shape m=%lld n=%lld k=%lld", name, (long long)m,
+              (long long)n, (long long)k);
+  M5K_REQUIRE(m <= 0x7FFFFFFF && n <= 0x7FFFFFFF, "%s: m or n exceeds int32", name);
+  return M5K_OK;
+}
+
+template <int MODE, int OUT_DT>
+int launch_plain(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
+                 hipStream_t st, const char* name) {
+  if (p.residual) {
+    return p.gate_map ? launch<MODE, M5K_BF16, EPI_NONE, EPI_TABLE, false>(a, b, m, n, k, p, st, name)
+                      : launch<MODE, M5K_BF16, EPI_NONE, EPI_VECTOR, false>(a, b, m, n, k, p, st, name);
+  }
+  return launch<MODE, OUT_DT, EPI_NONE, EPI_NONE, false>(a, b, m, n, k, p, st, name);
+}
+
+template <int OUT_DT>
+int launch_i8(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
+              hipStream_t st) {
+  const char* name = "m5k_gemm_i8";
+  if (p.bias) {
+    return p.bias_map ? launch<I8, OUT_DT, EPI_TABLE, EPI_NONE, false>(a, b, m, n, k, p, st, name)
+                      : launch<I8, OUT_DT, EPI_VECTOR, EPI_NONE, false>(a, b, m, n, k, p, st, name);
+  }
+  return launch_plain<I8, OUT_DT>(a, b, m, n, k, p, st, name);
+}
+
+}  // namespace detail
+}  // namespace gemm
+}  // namespace m5k
+

@@ -1,0 +1,188 @@
+// Block-Hadamard rotation (FP32 output) and fused rotation + per-row INT8 quantizer.
+//
+// rotate:  Y = (X * signs) blockdiag(H_B) in FP32 (hadamard.py:33-77).  Streaming
+//          kernel: every lane owns EPC consecutive elements, 2 (bf16) or 4 (fp32) bytes
+//          in and 4 bytes out per element, no LDS.
+// fused:   codes/scales of quantize(rotate(X), "int8") (hadamard_gemm.py:27-69 online
+//          path) with one workgroup per row; the rotated row stays in VGPRs between
+//          the row-peak reduction and the encode, so HBM sees 2K + K + 4 bytes per row.
+//          Codes equal the two-kernel composition bit for bit (same FP32 values).
+#include "hadamard_core.h"
+
+namespace m5k {
+namespace hadamard {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int DT, int B>
+__global__ __launch_bounds__(kThreads) void rotate_kernel(const void* __restrict__ x, int64_t total_chunks,
+                                                          int64_t k, const int8_t* __restrict__ signs,
+                                                          float* __restrict__ y) {
+  constexpr int EPC = Shape<B>::EPC;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const bool live = g < total_chunks;
+  const int64_t e = g * EPC;
+  float v[EPC];
+  if (live) {
+    load_signed<DT, EPC>(x, e, signs, e % k, v);
+  } else {
+#pragma unroll
+    for (int r = 0; r < EPC; ++r) v[r] = 0.0f;
+  }
+  butterflies<B>(v);  // every lane participates in the exchanges
+  if (live) {
+    float4* out = reinterpret_cast<float4*>(y + e);
+#pragma unroll
+    for (int t = 0; t < EPC / 4; ++t) out[t] = make_float4(v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]);
+  }
+}
+
+template <int DT, int B, int CPT>
+__global__ __launch_bounds__(kThreads) void rotate_quant_kernel(const void* __restrict__ x, int64_t k,
+                                                                const int8_t* __restrict__ signs,
+                                                                int8_t* __restrict__ q, float* __restrict__ scales) {
+  __shared__ float red[kThreads / 64];
+  constexpr int EPC = Shape<B>::EPC;
+  const int64_t row = blockIdx.x;
+  const int64_t nchunks = k / EPC;
+  float v[CPT][EPC];
+  float peak = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+    if (c < nchunks) {
+      load_signed<DT, EPC>(x, row * k + c * EPC, signs, c * EPC, v[i]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < EPC; ++r) v[i][r] = 0.0f;
+    }
+    butterflies<B>(v[i]);
+#pragma unroll
+    for (int r = 0; r < EPC; ++r) peak = fmaxf(peak, fabsf(v[i][r]));
+  }
+  peak = block_max<kThreads / 64>(peak, red);
+  const float scale = quant_scale<M5K_QUANT_INT8>(peak);
+  if (threadIdx.x == 0) scales[row] = scale;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+    if (c < nchunks) {
+      uint2* out = reinterpret_cast<uint2*>(q + row * k + c * EPC);
+#pragma unroll
+      for (int t = 0; t < EPC / 8; ++t) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          lo |= quant_encode<M5K_QUANT_INT8>(v[i][8 * t + b], scale) << (8 * b);
+          hi |= quant_encode<M5K_QUANT_INT8>(v[i][8 * t + 4 + b], scale) << (8 * b);
+        }
+        out[t] = make_uint2(lo, hi);
+      }
+    }
+  }
+}
+
+template <int DT, int B>
+int launch_rotate(const void* x, int64_t rows, int64_t k, const int8_t* signs, float* y, hipStream_t st) {
+  const int64_t total = rows * k / Shape<B>::EPC;
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  M5K_REQUIRE(blocks <= 0x7FFFFFFF, "m5k_hadamard_rotate: input too large");
+  rotate_kernel<DT, B><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st>>>(x, total, k, signs, y);
+  return launch_status("m5k_hadamard_rotate");
+}
+
+template <int DT, int B>
+int launch_rotate_quant(const void* x, int64_t rows, int64_t k, const int8_t* signs, int8_t* q, float* s,
+                        hipStream_t st) {
+  const int64_t per_thread = (k / Shape<B>::EPC + kThreads - 1) / kThreads;
+  const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
+  if (per_thread <= 1) rotate_quant_kernel<DT, B, 1><<<grid, block, 0, st>>>(x, k, signs, q, s);
+  else if (per_thread <= 2) rotate_quant_kernel<DT, B, 2><<<grid, block, 0, st>>>(x, k, signs, q, s);
+  else if (per_thread <= 4) rotate_quant_kernel<DT, B, 4><<<grid, block, 0, st>>>(x, k, signs, q, s);
+  else if (per_thread <= 8) rotate_quant_kernel<DT, B, 8><<<grid, block, 0, st>>>(x, k, signs, q, s);
+  else {
+    set_error("m5k_hadamard_quantize_rows: K=%lld exceeds the register-resident row limit %d", (long long)k,
+              8 * kThreads * Shape<B>::EPC);
+    return M5K_EINVAL;
+  }
+  return launch_status("m5k_hadamard_quantize_rows");
+}
+
+template <int DT, template <int, int> class Launcher, class... Args>
+int by_block(int block, Args... args) {
+  switch (block) {
+    case 32: return Launcher<DT, 32>::run(args...);
+    case 64: return Launcher<DT, 64>::run(args...);
+    case 128: return Launcher<DT, 128>::run(args...);
+    case 256: return Launcher<DT, 256>::run(args...);
+    case 512: return Launcher<DT, 512>::run(args...);
+    case 1024: return Launcher<DT, 1024>::run(args...);
+    default: set_error("unsupported Hadamard block %d", block); return M5K_EINVAL;
+  }
+}
+
+template <int DT, int B>
+struct RotateL {
+  static int run(const void* x, int64_t rows, int64_t k, const int8_t* signs, float* y, hipStream_t st) {
+    return launch_rotate<DT, B>(x, rows, k, signs, y, st);
+  }
+};
+
+template <int DT, int B>
+struct RotateQuantL {
+  static int run(const void* x, int64_t rows, int64_t k, const int8_t* signs, int8_t* q, float* s,
+                 hipStream_t st) {
+    return launch_rotate_quant<DT, B>(x, rows, k, signs, q, s, st);
+  }
+};
+
+int check_args(const void* x, int x_dtype, int64_t rows, int64_t k, int block, const int8_t* signs,
+               const char* name) {
+  M5K_REQUIRE(x && signs, "%s: null pointer", name);
+  M5K_REQUIRE(rows > 0 && k > 0, "%s: empty shape", name);
+  M5K_REQUIRE(block >= 32 && block <= 1024 && (block & (block - 1)) == 0, "%s: block %d not in {32..1024}", name,
+              block);
+  M5K_REQUIRE(k % block == 0, "%s: K=%lld not divisible by block %d", name, (long long)k, block);
+  M5K_REQUIRE(x_dtype == M5K_BF16 || x_dtype == M5K_F16 || x_dtype == M5K_F32, "%s: unsupported dtype %d", name,
+              x_dtype);
+  M5K_REQUIRE(aligned16(x) && (reinterpret_cast<uintptr_t>(signs) & 7u) == 0,
+              "%s: x must be 16-byte and signs 8-byte aligned", name);
+  return M5K_OK;
+}
+
+}  // namespace
+}  // namespace hadamard
+}  // namespace m5k
+
+using namespace m5k;
+using namespace m5k::hadamard;
+
+extern "C" int m5k_hadamard_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int block,
+                                   const int8_t* signs, float* y, void* stream) {
+  clear_error();
+  const char* name = "m5k_hadamard_rotate";
+  if (int rc = check_args(x, x_dtype, rows, k, block, signs, name)) return rc;
+  M5K_REQUIRE(y && aligned16(y), "%s: y must be a 16-byte aligned pointer", name);
+  hipStream_t st = as_stream(stream);
+  switch (x_dtype) {
+    case M5K_BF16: return by_block<M5K_BF16, RotateL>(block, x, rows, k, signs, y, st);
+    case M5K_F16: return by_block<M5K_F16, RotateL>(block, x, rows, k, signs, y, st);
+    default: return by_block<M5K_F32, RotateL>(block, x, rows, k, signs, y, st);
+  }
+}
+
+extern "C" int m5k_hadamard_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int block,
+                                          const int8_t* signs, int8_t* q, float* scales, void* stream) {
+  clear_error();
+  const char* name = "m5k_hadamard_quantize_rows";
+  if (int rc = check_args(x, x_dtype, rows, k, block, signs, name)) return rc;
+  M5K_REQUIRE(q && scales && (reinterpret_cast<uintptr_t>(q) & 7u) == 0, "%s: q must be 8-byte aligned", name);
+  M5K_REQUIRE(rows <= 0x7FFFFFFF, "%s: too many rows", name);
+  hipStream_t st = as_stream(stream);
+  switch (x_dtype) {
+    case M5K_BF16: return by_block<M5K_BF16, RotateQuantL>(block, x, rows, k, signs, q, scales, st);
+    case M5K_F16: return by_block<M5K_F16, RotateQuantL>(block, x, rows, k, signs, q, scales, st);
+    default: return by_block<M5K_F32, RotateQuantL>(block, x, rows, k, signs, q, scales, st);
+  }
+}

@@ -1,0 +1,110 @@
+// Signed block-Hadamard butterflies on wave64 register tiles.
+//
+// Transform (hadamard.py:33-45, shaders/hadamard.metal:6-26): for each block of B
+// consecutive elements of a row, v = x * sign, then log2(B) natural-order Sylvester
+// stages; at stride s the pair (i, i+s) (bit s of i clear) becomes (a+b, a-b), then
+// every value is multiplied once by the FP32 constant 1/sqrt(B).
+//
+// Register layout: a lane holds EPC = max(8, B/64) consecutive elements of a block, so
+// one block spans LPB = B/EPC <= 64 consecutive lanes.  Strides below EPC stay inside
+// a lane's registers; strides EPC..B/2 are lane-xor exchanges within the LPB-lane group
+// (the upper lane of a pair computes lower - upper).  Each stage output is one FP32
+// add or subtract of its two inputs, so the result is independent of which lane does
+// the work and bit-identical to a sequential FP32 evaluation of the same stages.
+#pragma once
+
+#include "m5k_common.h"
+
+namespace m5k {
+namespace hadamard {
+
+template <int B>
+struct Shape {
+  static_assert(B >= 32 && B <= 1024 && (B & (B - 1)) == 0, "block must be a power of two in [32,1024]");
+  static constexpr int EPC = B / 64 > 8 ? B / 64 : 8;  // elements per lane
+  static constexpr int LPB = B / EPC;                  // lanes per block
+};
+
+// FP32 nearest value of 1/sqrt(B) (the double 1/sqrt(B) rounded to float).
+template <int B>
+__device__ __forceinline__ constexpr float inv_sqrt_block() {
+  return B == 32    ? 0x1.6a09e6p-3f
+         : B == 64  ? 0x1.0p-3f
+         : B == 128 ? 0x1.6a09e6p-4f
+         : B == 256 ? 0x1.0p-4f
+         : B == 512 ? 0x1.6a09e6p-5f
+                    : 0x1.0p-5f;
+}
+
+// In-place transform of v[EPC] for the calling lane (all lanes of a block must call).
+template <int B>
+__device__ __forceinline__ void butterflies(float (&v)[Shape<B>::EPC]) {
+  constexpr int EPC = Shape<B>::EPC, LPB = Shape<B>::LPB;
+#pragma unroll
+  for (int s = 1; s < EPC; s <<= 1) {
+#pragma unroll
+    for (int base = 0; base < EPC; base += 2 * s) {
+#pragma unroll
+      for (int j = 0; j < s; ++j) {
+        const float a = v[base + j], c = v[base + j + s];
+        v[base + j] = a + c;
+        v[base + j + s] = a - c;
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 1; m < LPB; m <<= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int r = 0; r < EPC; ++r) {
+      const float peer = __shfl_xor(v[r], m, 64);
+      v[r] = upper ? peer - v[r] : v[r] + peer;
+    }
+  }
+  constexpr float inv = inv_sqrt_block<B>();
+#pragma unroll
+  for (int r = 0; r < EPC; ++r) v[r] = v[r] * inv;
+}
+
+// Load EPC consecutive elements of dtype DT starting at element index e (16-byte aligned
+// when the caller checked alignment) and apply the shared signs.
+template <int DT, int EPC>
+__device__ __forceinline__ void load_signed(const void* __restrict__ x, int64_t e, const int8_t* __restrict__ signs,
+                                            int64_t j, float (&v)[EPC]) {
+  constexpr int EB = dtype_bytes<DT>();
+  constexpr int NV = EPC * EB / 16;  // 16-byte vectors
+  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + e * EB);
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    const uint4 w = p[t];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (DT == M5K_F32) {
+        v[t * 4 + q] = __uint_as_float(ws[q]);
+      } else if constexpr (DT == M5K_BF16) {
+        v[t * 8 + 2 * q] = bf16_bits_to_f32(ws[q] & 0xFFFFu);
+        v[t * 8 + 2 * q + 1] = bf16_bits_to_f32(ws[q] >> 16);
+      } else {
+        v[t * 8 + 2 * q] = f16_bits_to_f32(ws[q] & 0xFFFFu);
+        v[t * 8 + 2 * q + 1] = f16_bits_to_f32(ws[q] >> 16);
+      }
+    }
+  }
+  // Signs are +-1: multiplication is an exact sign flip.
+  const uint2* sp = reinterpret_cast<const uint2*>(signs + j);
+#pragma unroll
+  for (int t = 0; t < EPC / 8; ++t) {
+    const uint2 s = sp[t];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t byte = ((q < 4 ? s.x : s.y) >> (8 * (q & 3))) & 0xFFu;
+      const float sg = static_cast<float>(static_cast<int8_t>(byte));
+      v[t * 8 + q] = v[t * 8 + q] * sg;
+    }
+  }
+}
+
+}  // namespace hadamard
+}  // namespace m5k

@@ -1,0 +1,160 @@
+// Shared device helpers and host-side error plumbing for libm5k.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "m5k.h"
+
+namespace m5k {
+
+// ---- host-side status --------------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+// Translate a launch's hipGetLastError() into the ABI status.
+int launch_status(const char* what);
+
+#define M5K_REQUIRE(cond, ...)          \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::m5k::set_error(__VA_ARGS__);    \
+      return M5K_EINVAL;                \
+    }                                   \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- element conversions (device) --------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// FP32 -> BF16 round to nearest even, the producer-side cast of the reference
+// (qk_rope_reference.py:37-42 bit formula; finite inputs).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  return __half2float(__ushort_as_half(static_cast<unsigned short>(bits16)));
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// Round an FP32 value through a storage dtype and back (the "O(...)" boundary).
+template <int DT>
+__device__ __forceinline__ float round_through(float v) {
+  if constexpr (DT == M5K_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  else if constexpr (DT == M5K_F16) return f16_bits_to_f32(f32_to_f16_bits(v));
+  else return v;
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, int64_t i) {
+  if constexpr (DT == M5K_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(base)[i]);
+  else if constexpr (DT == M5K_F16) return f16_bits_to_f32(static_cast<const uint16_t*>(base)[i]);
+  else return static_cast<const float*>(base)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
+  if constexpr (DT == M5K_BF16) static_cast<uint16_t*>(base)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else if constexpr (DT == M5K_F16) static_cast<uint16_t*>(base)[i] = (uint16_t)f32_to_f16_bits(v);
+  else static_cast<float*>(base)[i] = v;
+}
+
+template <int DT>
+constexpr int dtype_bytes() {
+  return DT == M5K_F32 ? 4 : 2;
+}
+
+// OCP FP8 E4M3 ("fn") encoder: nearest finite code, ties to even code,
+// saturating to 448 (code 126), sign taken from the sign bit.  Restates
+// numerics.fp8_encode (src/m5kernels/numerics.py:17-26) with exponent-field
+// extraction instead of a codebook search.  Finite input only.
+__device__ __forceinline__ uint32_t fp8_e4m3_encode(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = __uint_as_float(u & 0x7FFFFFFFu);
+  uint32_t bits;
+  if (!(a < 448.0f)) {
+    bits = 126u;
+  } else if (a < 0.015625f) {  // below 2^-6: subnormal grid m * 2^-9, exact scaling
+    bits = static_cast<uint32_t>(rintf(a * 512.0f));
+  } else {
+    int e = static_cast<int>((u >> 23) & 0xFFu) - 127;  // floor(log2 a), a normal
+    float scaled = __uint_as_float(static_cast<uint32_t>(127 + 3 - e) << 23);  // 2^(3-e)
+    int qm = static_cast<int>(rintf(a * scaled));                              // in [8,16]
+    if (qm == 16) { qm = 8; ++e; }
+    bits = static_cast<uint32_t>(((e + 7) << 3) + (qm - 8));
+    bits = bits > 126u ? 126u : bits;
+  }
+  return sign | bits;
+}
+
+// Per-row quantization of one value given the row scale (IEEE FP32 division, then
+// round-half-even and clamp for INT8; E4M3 encode for FP8).
+template <int MODE>
+__device__ __forceinline__ uint32_t quant_encode(float x, float scale) {
+  const float z = x / scale;
+  if constexpr (MODE == M5K_QUANT_FP8) {
+    return fp8_e4m3_encode(z);
+  } else {
+    const float r = fminf(fmaxf(rintf(z), -127.0f), 127.0f);
+    return static_cast<uint32_t>(static_cast<int>(r)) & 0xFFu;
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ float quant_scale(float peak) {
+  return peak == 0.0f ? 1.0f : peak / (MODE == M5K_QUANT_FP8 ? 448.0f : 127.0f);
+}
+
+// ---- wave64 reductions -------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m <= 32; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Block-wide reductions over NWAVES waves via LDS; every thread gets the result.
+template <int NWAVES>
+__device__ __forceinline__ float block_max(float v, float* lds) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int w = 1; w < NWAVES; ++w) r = fmaxf(r, lds[w]);
+  __syncthreads();
+  return r;
+}
+
+template <int NWAVES>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int w = 1; w < NWAVES; ++w) r += lds[w];
+  __syncthreads();
+  return r;
+}
+
+}  // namespace m5k

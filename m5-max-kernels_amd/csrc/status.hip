@@ -1,0 +1,35 @@
+// Thread-local error message and launch-status helpers for the C ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "m5k_common.h"
+
+namespace m5k {
+
+static thread_local char g_error[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_error[0] = 0; }
+
+int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return M5K_ELAUNCH;
+  }
+  return M5K_OK;
+}
+
+}  // namespace m5k
+
+extern "C" const char* m5k_last_error(void) { return m5k::g_error; }
+
+extern "C" int m5k_abi_version(void) { return 100; }

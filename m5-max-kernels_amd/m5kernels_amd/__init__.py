@@ -1,0 +1,18 @@
+"""m5kernels_amd: the quantized projection hot path of m5-max-kernels on MI355X (gfx950).
+
+Python op contracts mirror the reference package ``m5kernels`` (quantize, gemm, rotate,
+...) on torch tensors; every computation runs in libm5k.so, hand-written HIP kernels
+behind a C ABI (include/m5k.h).  There is no CPU fallback.
+"""
+
+from .hip import gemm, gemm_i8_accumulators, quantize
+from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
+
+__all__ = [
+    "quantize",
+    "gemm",
+    "gemm_i8_accumulators",
+    "rotate",
+    "rotate_quantize",
+    "SUPPORTED_BLOCK_SIZES",
+]

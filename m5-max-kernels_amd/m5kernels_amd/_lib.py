@@ -1,0 +1,109 @@
+"""ctypes binding of libm5k.so and the torch-tensor plumbing around it.
+
+PyTorch-ROCm supplies device memory and the current HIP stream; every compute call
+goes through the C ABI declared in include/m5k.h.  There is no fallback: if the
+library is missing or a tensor is not on a ROCm device, the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libm5k.so"
+
+F32, F16, BF16, I8, U8, I32 = 0, 1, 2, 3, 4, 5
+QUANT_INT8, QUANT_FP8 = 0, 1
+NORM_RMS, NORM_LAYER = 0, 1
+
+_DTYPE_CODES = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.int8: I8,
+    torch.uint8: U8,
+    torch.int32: I32,
+}
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+
+# name -> argtypes (restype is int status unless noted)
+SIGNATURES = {
+    "m5k_quantize_rows": [_p, _i32, _i64, _i64, _i32, _p, _p, _p],
+    "m5k_gemm_i8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p],
+    "m5k_gemm_i8_acc": [_p, _p, _i64, _i64, _i64, _p, _p],
+    "m5k_gemm_f8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p],
+    "m5k_gemm_float": [_p, _p, _i32, _i64, _i64, _i64, _p, _i32, _p, _p, _p, _p],
+    "m5k_hadamard_rotate": [_p, _i32, _i64, _i64, _i32, _p, _p, _p],
+    "m5k_hadamard_quantize_rows": [_p, _i32, _i64, _i64, _i32, _p, _p, _p, _p],
+}
+
+_LIB = None
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load libm5k.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    target = Path(path) if path is not None else LIB_PATH
+    if not target.exists():
+        raise RuntimeError(
+            f"{target} is missing: build it with `python -m m5kernels_amd.build` "
+            "(or __graft_entry__.build()); there is no CPU fallback"
+        )
+    lib = ctypes.CDLL(str(target))
+    lib.m5k_last_error.restype = ctypes.c_char_p
+    lib.m5k_last_error.argtypes = []
+    lib.m5k_abi_version.restype = ctypes.c_int
+    lib.m5k_abi_version.argtypes = []
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"{name} failed ({rc}): {lib.m5k_last_error().decode(errors='replace')}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+def device_tensor(t: torch.Tensor, name: str) -> torch.Tensor:
+    """Contiguous view of a ROCm device tensor (copies strided inputs, never mutates)."""
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a ROCm device tensor (got {t.device}); there is no CPU path")
+    return t.contiguous()
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def aligned_device_tensor(t: torch.Tensor, name: str) -> torch.Tensor:
+    """Like device_tensor, but also guarantees a 16-byte aligned base (vector kernels)."""
+    t = device_tensor(t, name)
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t

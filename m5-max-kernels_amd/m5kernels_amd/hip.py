@@ -1,0 +1,257 @@
+"""Quantizer and linear-layer op contracts on torch tensors, backed by libm5k.so.
+
+Drop-in mirror of the reference's ``metal.quantize`` / ``metal.gemm``
+(src/m5kernels/metal.py:27-44, 158-269): same names, positional/keyword
+signatures, defaults, argument meaning and exception types.  Inputs are never
+mutated; outputs are freshly allocated on the input's device and computed on
+the current HIP stream.
+
+Differences that follow from the platform, not the contract:
+
+* ``tile=(TM, TN, groups, swizzle)`` names an Apple threadgroup tiling.  It is
+  unpacked (so malformed tuples fail as in the reference) but the MI355X kernel
+  always uses its own 256x256 MFMA tile with an XCD-aware raster.
+* ``tag`` only specialized the Metal kernel name; it is accepted and ignored.
+* ``mode="mxint8"`` and ``mode="fp32"`` are outside the MI355X hot path and raise
+  NotImplementedError.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_QUANT_MODES = {"int8": _lib.QUANT_INT8, "fp8": _lib.QUANT_FP8}
+_FLOAT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+# metal.py:59-66 dtype table (the KeyError for unknown modes is preserved).
+_MODE_DTYPES = {
+    "fp16": torch.float16,
+    "bf16": torch.bfloat16,
+    "fp32": torch.float32,
+    "int8": torch.int8,
+    "mxint8": torch.int8,
+    "fp8": torch.uint8,
+}
+
+
+def quantize(x, mode, tag="packed"):
+    """Return (codes, scales) of symmetric per-row quantization of X[rows, K].
+
+    INT8: int8 codes in [-127, 127], scale = max|row| / 127 (1 for an all-zero row),
+    code = rint_even(x / scale).  FP8: uint8 OCP E4M3 codes of x / scale with
+    scale = max|row| / 448.  Mirrors metal.quantize (metal.py:27-44).
+    """
+    rows, k = x.shape
+    if mode == "mxint8":
+        if k % 32:
+            raise ValueError("MXINT8 requires K divisible by 32")
+        raise NotImplementedError("MXINT8 block quantization is not part of the MI355X hot path")
+    if mode not in _QUANT_MODES:
+        raise ValueError(f"unknown quantization mode: {mode!r}")
+    if x.dtype not in _FLOAT_DTYPES:
+        raise ValueError("quantization input must be float16, bfloat16 or float32")
+    if rows == 0 or k == 0:
+        raise ValueError("quantization input must be nonempty")
+    x = _lib.device_tensor(x, "x")
+    q = torch.empty((rows, k), dtype=torch.uint8 if mode == "fp8" else torch.int8, device=x.device)
+    s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    _lib.call(
+        "m5k_quantize_rows",
+        _lib.ptr(x),
+        _lib.dtype_code(x),
+        rows,
+        k,
+        _QUANT_MODES[mode],
+        _lib.ptr(q),
+        _lib.ptr(s),
+        _lib.stream_of(x),
+    )
+    return q, s
+
+
+def _check_vector(t, n, dtype, message):
+    if t is None or tuple(t.shape) != (n,) or t.dtype != dtype:
+        raise ValueError(message)
+
+
+def gemm(
+    a,
+    b,
+    mode="bf16",
+    tile=(64, 64, 4, 1),
+    a_scales=None,
+    b_scales=None,
+    output_dtype=None,
+    bias=None,
+    bias_row_map=None,
+    residual=None,
+    gate=None,
+    gate_row_map=None,
+):
+    """A[M,K] @ B[N,K].T with INT32 (int8) or FP32 (fp8/bf16/fp16) accumulation.
+
+    Quantized modes apply ``O(float(acc) * a_scales[m] * b_scales[n])`` in FP32, left to
+    right.  INT8 optionally adds an FP32 bias [N] (or [P,N] selected by int32
+    bias_row_map[M]) before the output cast.  INT8/BF16 optionally fuse a gated residual
+    update ``bf16(float(residual) + float(bf16(branch)) * float(gate))`` (gate [N] or
+    [P,N] with gate_row_map[M]); that requires BF16 output and cannot be combined with
+    a bias.  output_dtype defaults to float32.  Mirrors metal.gemm (metal.py:158-269).
+    """
+    m, k = a.shape
+    n, kb = b.shape
+    if k != kb:
+        raise ValueError("K mismatch")
+    if mode == "fp8" and k % 128:
+        raise NotImplementedError("FP8 requires K/row stride divisible by 128; padding is not implicit")
+    if mode == "int8" and k > 133144:
+        raise NotImplementedError("INT32 worst-case overflow bound exceeded")
+    gated = residual is not None or gate is not None or gate_row_map is not None
+    if gated:
+        if residual is None or gate is None:
+            raise ValueError("gated GEMM requires both residual and gate")
+        if mode not in {"int8", "bf16"}:
+            raise NotImplementedError("gated GEMM supports INT8 and BF16 only")
+        if output_dtype is None or output_dtype != torch.bfloat16:
+            raise NotImplementedError("gated GEMM requires explicit BF16 output_dtype")
+        if bias is not None or bias_row_map is not None:
+            raise NotImplementedError("combining GEMM bias and gated residual is unsupported")
+        if tuple(residual.shape) != (m, n) or residual.dtype != torch.bfloat16:
+            raise ValueError("residual must have BF16 dtype and shape [M,N]")
+        if gate.dtype != torch.bfloat16:
+            raise ValueError("gate must have BF16 dtype")
+        if gate_row_map is None:
+            if tuple(gate.shape) != (n,):
+                raise ValueError("gate must have shape [N] without gate_row_map")
+        else:
+            if gate.dim() != 2 or not all(gate.shape) or gate.shape[1] != n:
+                raise ValueError("mapped gate must have nonempty shape [P,N]")
+            if tuple(gate_row_map.shape) != (m,) or gate_row_map.dtype != torch.int32:
+                raise ValueError("gate_row_map must be an int32 vector of length M")
+        expected_dtype = torch.int8 if mode == "int8" else torch.bfloat16
+        if a.dtype != expected_dtype or b.dtype != expected_dtype:
+            raise ValueError("gated GEMM operand dtypes must match the declared mode")
+        if mode == "int8" and (
+            a_scales is None
+            or b_scales is None
+            or tuple(a_scales.shape) != (m,)
+            or tuple(b_scales.shape) != (n,)
+            or a_scales.dtype != torch.float32
+            or b_scales.dtype != torch.float32
+        ):
+            raise ValueError("gated INT8 GEMM requires float32 scales with shapes [M] and [N]")
+    if bias is None:
+        if bias_row_map is not None:
+            raise ValueError("bias_row_map requires a bias table")
+    else:
+        if mode != "int8":
+            raise NotImplementedError("optional GEMM bias currently supports INT8 only")
+        if bias.dtype != torch.float32:
+            raise ValueError("bias must have float32 dtype")
+        if bias_row_map is None:
+            if tuple(bias.shape) != (n,):
+                raise ValueError("bias must have shape [N] without bias_row_map")
+        else:
+            if bias.dim() != 2 or not all(bias.shape) or bias.shape[1] != n:
+                raise ValueError("mapped bias must have nonempty shape [P,N]")
+            if tuple(bias_row_map.shape) != (m,) or bias_row_map.dtype != torch.int32:
+                raise ValueError("bias_row_map must be an int32 vector of length M")
+    tm, tn, groups, swizzle = tile
+    operand_dtype = _MODE_DTYPES[mode]  # KeyError for an unknown mode, as in metal.py:59-66
+    if mode in {"int8", "fp8", "mxint8"}:
+        if a_scales is None or b_scales is None:
+            raise ValueError("scales required")
+    if mode in {"mxint8", "fp32"}:
+        raise NotImplementedError(f"{mode} GEMM is not part of the MI355X hot path")
+    if a.dtype != operand_dtype or b.dtype != operand_dtype:
+        raise ValueError(f"{mode} GEMM requires {operand_dtype} operands")
+    if m == 0 or n == 0 or k == 0:
+        raise ValueError("GEMM operands must be nonempty")
+    out_dtype = output_dtype or torch.float32
+    if out_dtype not in _FLOAT_DTYPES:
+        raise ValueError("output_dtype must be float16, bfloat16 or float32")
+
+    a = _lib.device_tensor(a, "a")
+    b = _lib.device_tensor(b, "b")
+    c = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    out_code = _lib.dtype_code(c)
+    stream = _lib.stream_of(a)
+    if residual is not None:
+        residual = _lib.device_tensor(residual, "residual")
+        gate = _lib.device_tensor(gate, "gate")
+        gate_row_map = None if gate_row_map is None else _lib.device_tensor(gate_row_map, "gate_row_map")
+    if mode in {"int8", "fp8"}:
+        _check_vector(a_scales, m, torch.float32, "a_scales must be a float32 vector of length M")
+        _check_vector(b_scales, n, torch.float32, "b_scales must be a float32 vector of length N")
+        a_scales = _lib.device_tensor(a_scales, "a_scales")
+        b_scales = _lib.device_tensor(b_scales, "b_scales")
+    if mode == "int8":
+        if bias is not None:
+            bias = _lib.device_tensor(bias, "bias")
+            bias_row_map = None if bias_row_map is None else _lib.device_tensor(bias_row_map, "bias_row_map")
+        _lib.call(
+            "m5k_gemm_i8",
+            _lib.ptr(a),
+            _lib.ptr(b),
+            m,
+            n,
+            k,
+            _lib.ptr(a_scales),
+            _lib.ptr(b_scales),
+            _lib.ptr(c),
+            out_code,
+            _lib.ptr(bias),
+            _lib.ptr(bias_row_map),
+            _lib.ptr(residual),
+            _lib.ptr(gate),
+            _lib.ptr(gate_row_map),
+            stream,
+        )
+    elif mode == "fp8":
+        _lib.call(
+            "m5k_gemm_f8",
+            _lib.ptr(a),
+            _lib.ptr(b),
+            m,
+            n,
+            k,
+            _lib.ptr(a_scales),
+            _lib.ptr(b_scales),
+            _lib.ptr(c),
+            out_code,
+            stream,
+        )
+    else:
+        _lib.call(
+            "m5k_gemm_float",
+            _lib.ptr(a),
+            _lib.ptr(b),
+            _lib.dtype_code(a),
+            m,
+            n,
+            k,
+            _lib.ptr(c),
+            out_code,
+            _lib.ptr(residual),
+            _lib.ptr(gate),
+            _lib.ptr(gate_row_map),
+            stream,
+        )
+    return c
+
+
+def gemm_i8_accumulators(a, b):
+    """Raw INT32 accumulators sum_k a[m,k]*b[n,k] of the W8A8 main loop (parity hook)."""
+    m, k = a.shape
+    n, kb = b.shape
+    if k != kb:
+        raise ValueError("K mismatch")
+    if a.dtype != torch.int8 or b.dtype != torch.int8:
+        raise ValueError("accumulator hook requires int8 operands")
+    if k > 133144:
+        raise NotImplementedError("INT32 worst-case overflow bound exceeded")
+    a = _lib.device_tensor(a, "a")
+    b = _lib.device_tensor(b, "b")
+    acc = torch.empty((m, n), dtype=torch.int32, device=a.device)
+    _lib.call("m5k_gemm_i8_acc", _lib.ptr(a), _lib.ptr(b), m, n, k, _lib.ptr(acc), _lib.stream_of(a))
+    return acc

@@ -1,0 +1,118 @@
+"""Host-side op contracts (CPU): the same exception type for the same condition as the
+reference's Python ops, raised before any device work, and no silent CPU path."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from m5kernels_amd import gemm, quantize, rotate, rotate_quantize
+
+
+def test_quantize_rejections():
+    with pytest.raises(ValueError):
+        quantize(torch.zeros(8), "int8")  # not [rows, K]
+    with pytest.raises(ValueError, match="unknown"):
+        quantize(torch.zeros(2, 8), "int4")
+    with pytest.raises(ValueError, match="MXINT8 requires K divisible by 32"):
+        quantize(torch.zeros(2, 40), "mxint8")
+    with pytest.raises(NotImplementedError):
+        quantize(torch.zeros(2, 64), "mxint8")
+    with pytest.raises(ValueError, match="float16, bfloat16 or float32"):
+        quantize(torch.zeros(2, 8, dtype=torch.int8), "int8")
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    with pytest.raises(ValueError, match="ROCm device"):
+        quantize(torch.ones(2, 8), "int8")
+    with pytest.raises(ValueError, match="ROCm device"):
+        gemm(torch.ones(2, 8, dtype=torch.bfloat16), torch.ones(3, 8, dtype=torch.bfloat16), "bf16")
+
+
+def _i8(m, k):
+    return torch.zeros(m, k, dtype=torch.int8)
+
+
+def test_gemm_shape_and_mode_rejections():
+    with pytest.raises(ValueError, match="K mismatch"):
+        gemm(_i8(2, 8), _i8(3, 9), "int8")
+    with pytest.raises(NotImplementedError, match="stride"):  # reference test_metal.py:137-143
+        gemm(torch.zeros(2, 96, dtype=torch.uint8), torch.zeros(3, 96, dtype=torch.uint8), "fp8")
+    with pytest.raises(NotImplementedError, match="overflow"):
+        gemm(_i8(1, 133145), _i8(1, 133145), "int8")
+    with pytest.raises(ValueError, match="scales required"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8")
+    with pytest.raises(KeyError):
+        gemm(_i8(2, 8), _i8(3, 8), "int4")
+    with pytest.raises(NotImplementedError):
+        gemm(torch.zeros(2, 8), torch.zeros(3, 8), "fp32")
+    with pytest.raises(ValueError):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", tile=(64, 64))
+
+
+def test_gemm_epilogue_rejections():
+    sa, sb = torch.ones(2), torch.ones(3)
+    kw = dict(a_scales=sa, b_scales=sb)
+    res = torch.zeros(2, 3, dtype=torch.bfloat16)
+    gate = torch.zeros(3, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="both residual and gate"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", residual=res, output_dtype=torch.bfloat16, **kw)
+    with pytest.raises(NotImplementedError, match="INT8 and BF16"):
+        gemm(torch.zeros(2, 128, dtype=torch.uint8), torch.zeros(3, 128, dtype=torch.uint8), "fp8",
+             residual=res, gate=gate, **kw)
+    with pytest.raises(NotImplementedError, match="explicit BF16"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", residual=res, gate=gate, **kw)
+    with pytest.raises(NotImplementedError, match="combining"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", residual=res, gate=gate, bias=torch.zeros(3),
+             output_dtype=torch.bfloat16, **kw)
+    with pytest.raises(ValueError, match="residual must"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", residual=res.float(), gate=gate, output_dtype=torch.bfloat16, **kw)
+    with pytest.raises(ValueError, match="gate must have shape"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", residual=res, gate=gate[:2], output_dtype=torch.bfloat16, **kw)
+    with pytest.raises(ValueError, match="gate_row_map"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", residual=res, gate=torch.zeros(4, 3, dtype=torch.bfloat16),
+             gate_row_map=torch.zeros(2, dtype=torch.int64), output_dtype=torch.bfloat16, **kw)
+    with pytest.raises(ValueError, match="bias_row_map requires"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", bias_row_map=torch.zeros(2, dtype=torch.int32), **kw)
+    with pytest.raises(NotImplementedError, match="INT8 only"):
+        gemm(torch.zeros(2, 8, dtype=torch.bfloat16), torch.zeros(3, 8, dtype=torch.bfloat16), "bf16",
+             bias=torch.zeros(3))
+    with pytest.raises(ValueError, match="float32"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", bias=torch.zeros(3, dtype=torch.float16), **kw)
+    with pytest.raises(ValueError, match="shape \\[N\\]"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", bias=torch.zeros(4), **kw)
+    with pytest.raises(ValueError, match="mapped bias"):
+        gemm(_i8(2, 8), _i8(3, 8), "int8", bias=torch.zeros(4, 2), bias_row_map=torch.zeros(2, dtype=torch.int32),
+             **kw)
+
+
+@pytest.mark.parametrize("fn", [rotate, rotate_quantize])
+def test_hadamard_rejections(fn):
+    x = torch.zeros(3, 768)
+    signs = torch.ones(768, dtype=torch.int8)
+    for block, error, message in [
+        (33, ValueError, "power of two"),
+        (2.0, ValueError, "power of two"),
+        (True, ValueError, "power of two"),
+        (2048, NotImplementedError, "supported block sizes"),
+        (16, NotImplementedError, "supported block sizes"),
+        (512, NotImplementedError, "divisible"),
+    ]:
+        with pytest.raises(error, match=message):
+            fn(x, block, signs)
+    with pytest.raises(ValueError, match="signs"):
+        fn(x, 256, torch.ones(768))
+    with pytest.raises(ValueError, match="signs"):
+        fn(x, 256, torch.ones(767, dtype=torch.int8))
+    with pytest.raises(ValueError, match="shape"):
+        fn(torch.zeros(0, 768), 256, signs)
+    with pytest.raises(ValueError, match="dtype"):
+        fn(torch.zeros(3, 768, dtype=torch.int32), 256, signs)
+
+
+def test_rotate_implementation_switch():
+    x, signs = torch.zeros(3, 256), torch.ones(256, dtype=torch.int8)
+    with pytest.raises(NotImplementedError):
+        rotate(x, 256, signs, implementation="mlx")
+    with pytest.raises(ValueError, match="unknown Hadamard implementation"):
+        rotate(x, 256, signs, implementation="cuda")

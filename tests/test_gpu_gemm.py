@@ -1,0 +1,214 @@
+"""GPU parity of the MFMA GEMMs (m5k_gemm_i8 / _i8_acc / _f8 / _float).
+
+Bars: INT32 accumulators bit-exact; W8A8 BF16/FP32 outputs
+bit-exact against the oracle's FP32 epilogue (hence well within 1 bf16 ulp); FP8 and
+float modes within the reference's rel-L2 gate 0.008 of float64 (tests/test_metal.py:85-112
+of the reference) and rel-L2 1e-3 of the float64 product for FP32 output.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits_of, np_of
+from m5kernels_amd import gemm, gemm_i8_accumulators, quantize
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 33, 64), (127, 65, 96), (65, 17, 257), (256, 1024, 1024), (300, 520, 1000), (513, 260, 4096)]
+
+
+def _codes(m, n, k, seed=83, bound=127):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-bound, bound + 1, size=(m, k), dtype=np.int8)
+    b = rng.integers(-bound, bound + 1, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(0.01, 0.13, size=m).astype(np.float32)
+    sb = rng.uniform(0.02, 0.17, size=n).astype(np.float32)
+    return a, b, sa, sb
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_int32_accumulators_bit_exact(shape, device):
+    m, n, k = shape
+    a, b, _, _ = _codes(m, n, k)
+    acc = gemm_i8_accumulators(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
+    np.testing.assert_array_equal(np_of(acc), ref.c_gemm_i8_acc(a, b))
+
+
+def test_int32_accumulators_worst_case_magnitude(device):
+    m, n, k = 64, 96, 133144 // 8  # |acc| = 127^2 * K stays exact
+    a = np.full((m, k), -127, np.int8)
+    b = np.full((n, k), -127, np.int8)
+    b[1::2] = 127
+    acc = gemm_i8_accumulators(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
+    expected = np.where(np.arange(n) % 2 == 0, 127 * 127 * k, -127 * 127 * k)
+    np.testing.assert_array_equal(np_of(acc), np.broadcast_to(expected, (m, n)))
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("out", ["bf16", "fp32"])
+def test_w8a8_epilogue_bit_exact(shape, out, device):
+    m, n, k = shape
+    a, b, sa, sb = _codes(m, n, k)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    y = gemm(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device), "int8",
+             a_scales=torch.from_numpy(sa).to(device), b_scales=torch.from_numpy(sb).to(device), output_dtype=dt)
+    expected = ref.c_i8_epilogue(ref.c_gemm_i8_acc(a, b), sa, sb, out=out)
+    got = bits_of(y) if out == "bf16" else np_of(y)
+    np.testing.assert_array_equal(got, expected)
+
+
+def test_online_w8a8_config1_bit_exact(device):
+    """A bf16 [256,1024] ~N(0,1), W bf16 [1024,1024] ~N(0,0.02), seed 0."""
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((256, 1024), dtype=np.float32)
+    w = rng.standard_normal((1024, 1024), dtype=np.float32) * np.float32(0.02)
+    at = torch.from_numpy(a).to(device).to(torch.bfloat16)
+    wt = torch.from_numpy(w).to(device).to(torch.bfloat16)
+    wq, ws = quantize(wt, "int8")
+    aq, sa = quantize(at, "int8")
+    y = gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
+    expected = ref.c_w8a8_linear_bf16(bits_of(at), np_of(wq), np_of(ws))
+    np.testing.assert_array_equal(bits_of(y), expected)
+    # quality vs the float64 product of the bf16 operands (reference gate 0.05)
+    exact = at.double().cpu().numpy() @ wt.double().cpu().numpy().T
+    assert ref.metrics(y.float().cpu().numpy(), exact)["relative_l2"] < 0.05
+
+
+def test_ffn_down_full_size_sampled_rows_bit_exact(device):
+    """BASELINE FFN-down W8A8 at full size: every output of 32 sampled rows bit-exact."""
+    g = torch.Generator(device="cpu").manual_seed(29)
+    a = torch.randn((4096, 16384), generator=g)
+    a[:, ::1024] *= 50
+    w = torch.randn((4096, 16384), generator=g) * 0.02
+    at, wt = a.to(device).to(torch.bfloat16), w.to(device).to(torch.bfloat16)
+    wq, ws = quantize(wt, "int8")
+    aq, sa = quantize(at, "int8")
+    y = gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
+    rows = ref.sample_indices(4096)
+    aq_rows = np_of(aq)[rows]
+    acc = ref.c_gemm_i8_acc(aq_rows, np_of(wq))
+    expected = ref.c_i8_epilogue(acc, np_of(sa)[rows], np_of(ws))
+    np.testing.assert_array_equal(bits_of(y)[rows], expected)
+    # Size-independent property on the whole output: finite, and the row sums of the
+    # INT32 accumulators equal A_q . (sum of W_q rows) (linearity, exact in int64).
+    # Every partial sum is an integer below 2^53, so float64 is exact in any order.
+    accs = gemm_i8_accumulators(aq, wq)
+    lhs = accs.to(torch.float64).sum(dim=1)
+    rhs = aq.to(torch.float64) @ wq.to(torch.float64).sum(dim=0)
+    assert torch.equal(lhs, rhs)
+    assert torch.isfinite(y.float()).all()
+
+
+@pytest.mark.parametrize("mapped", [False, True])
+@pytest.mark.parametrize("shape", [(1, 17, 128), (7, 33, 256), (65, 67, 257)])
+def test_bias_epilogue_bit_exact(shape, mapped, device):
+    m, n, k = shape
+    a, b, sa, sb = _codes(m, n, k, bound=17)
+    rng = np.random.default_rng(97)
+    bias = rng.uniform(-1.5, 1.5, size=(4, n) if mapped else n).astype(np.float32)
+    row_map = (np.arange(m, dtype=np.int32) * 3 + 1) % 4 if mapped else None
+    y = gemm(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device), "int8", (32, 64, 4, 8),
+             a_scales=torch.from_numpy(sa).to(device), b_scales=torch.from_numpy(sb).to(device),
+             output_dtype=torch.bfloat16, bias=torch.from_numpy(bias).to(device),
+             bias_row_map=None if row_map is None else torch.from_numpy(row_map).to(device))
+    expected = ref.c_i8_epilogue(ref.c_gemm_i8_acc(a, b), sa, sb, bias=bias, bias_row_map=row_map)
+    np.testing.assert_array_equal(bits_of(y), expected)
+
+
+def test_bias_before_bf16_rounding_kat(kats, device):
+    kat = kats["gemm_bias_before_bf16_rounding"]
+    a = torch.zeros(kat["a_shape"], dtype=torch.int8, device=device)
+    b = torch.zeros(kat["b_shape"], dtype=torch.int8, device=device)
+    a[:, 0] = 1
+    b[:, 0] = 1
+    y = gemm(a, b, "int8", a_scales=torch.full((a.shape[0],), kat["a_scale"], device=device),
+             b_scales=torch.full((b.shape[0],), kat["b_scale"], device=device),
+             bias=torch.full((b.shape[0],), kat["bias"], device=device), output_dtype=torch.bfloat16)
+    np.testing.assert_array_equal(y.float().cpu().numpy(), np.float32(kat["expected"]))
+
+
+@pytest.mark.parametrize("mapped", [False, True])
+@pytest.mark.parametrize("mode", ["int8", "bf16"])
+def test_gated_epilogue(mode, mapped, device):
+    m, n, k = 65, 130, 257
+    rng = np.random.default_rng(61)
+    res = torch.from_numpy(rng.standard_normal((m, n), dtype=np.float32)).to(device).to(torch.bfloat16)
+    gate = torch.from_numpy(rng.uniform(-0.7, 0.7, size=(3, n) if mapped else n).astype(np.float32))
+    gate = gate.to(device).to(torch.bfloat16)
+    gmap = torch.from_numpy((np.arange(m, dtype=np.int32) * 7) % 3).to(device) if mapped else None
+    if mode == "int8":
+        a, b, sa, sb = _codes(m, n, k)
+        args = (torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
+        kw = dict(a_scales=torch.from_numpy(sa).to(device), b_scales=torch.from_numpy(sb).to(device))
+        y = gemm(*args, "int8", output_dtype=torch.bfloat16, residual=res, gate=gate, gate_row_map=gmap, **kw)
+        expected = ref.c_i8_epilogue(ref.c_gemm_i8_acc(a, b), sa, sb, residual_bits=bits_of(res),
+                                     gate_bits=bits_of(gate), gate_row_map=None if gmap is None else np_of(gmap))
+        np.testing.assert_array_equal(bits_of(y), expected)
+        staged = gemm(*args, "int8", output_dtype=torch.bfloat16, **kw)
+    else:
+        at = torch.randn(m, k, device=device).to(torch.bfloat16)
+        bt = torch.randn(n, k, device=device).to(torch.bfloat16)
+        y = gemm(at, bt, "bf16", output_dtype=torch.bfloat16, residual=res, gate=gate, gate_row_map=gmap)
+        staged = gemm(at, bt, "bf16", output_dtype=torch.bfloat16)
+    # Gated epilogue == staged bf16 branch followed by the FP32 gated add (bitwise).
+    g = gate if gmap is None else gate[gmap.long()]
+    manual = (res.float() + staged.float() * g.float()).to(torch.bfloat16)
+    np.testing.assert_array_equal(bits_of(y), bits_of(manual))
+
+
+@pytest.mark.parametrize("shape", [(1, 33, 128), (127, 65, 256), (300, 520, 1024), (256, 1024, 1024)])
+def test_fp8_gemm(shape, device):
+    m, n, k = shape
+    rng = np.random.default_rng(5)
+    a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(torch.bfloat16)
+    b = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device).to(torch.bfloat16)
+    aq, sa = quantize(a, "fp8")
+    bq, sb = quantize(b, "fp8")
+    decoded = (ref.dequantize(np_of(aq), np_of(sa), "fp8").astype(np.float64)
+               @ ref.dequantize(np_of(bq), np_of(sb), "fp8").astype(np.float64).T)
+    y32 = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb)
+    assert y32.dtype == torch.float32
+    assert ref.metrics(np_of(y32), decoded)["relative_l2"] < 1e-5
+    y = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb, output_dtype=torch.bfloat16)
+    assert ref.metrics(y.float().cpu().numpy(), decoded)["relative_l2"] < 0.008
+    # bf16 output is the RNE cast of an FP32 value within 1e-5 of the fp32 output: at most one ulp apart
+    diff = np.abs(bits_of(y).astype(np.int32) - ref.f32_to_bf16_bits(np_of(y32)).astype(np.int32))
+    assert diff.max() <= 1
+
+
+def test_fp8_ones_kat(kats, device):
+    kat = kats["fp8_ones_gemm"]
+    aq, sa = quantize(torch.ones(kat["a_shape"], device=device), "fp8")
+    bq, sb = quantize(torch.ones(kat["b_shape"], device=device), "fp8")
+    y = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb)
+    np.testing.assert_allclose(np_of(y), kat["expected"], rtol=1e-5)
+
+
+@pytest.mark.parametrize("mode", ["bf16", "fp16"])
+@pytest.mark.parametrize("shape", [(1, 33, 64), (127, 65, 96), (65, 17, 257), (300, 520, 1024)])
+def test_float_gemm(mode, shape, device):
+    m, n, k = shape
+    rng = np.random.default_rng(5)
+    dt = torch.float16 if mode == "fp16" else torch.bfloat16
+    a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(dt)
+    b = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device).to(dt)
+    expected = a.double().cpu().numpy() @ b.double().cpu().numpy().T
+    y = gemm(a, b, mode, output_dtype=dt)
+    assert ref.metrics(y.float().cpu().numpy(), expected)["relative_l2"] < 0.008
+    y32 = gemm(a, b, mode)
+    assert ref.metrics(np_of(y32), expected)["relative_l2"] < 1e-5
+
+
+def test_repeat_runs_identical(device):
+    """Deterministic output across launches (no LDS races in the main loop)."""
+    a, b, sa, sb = _codes(513, 777, 2048)
+    args = [torch.from_numpy(t).to(device) for t in (a, b)]
+    kw = dict(a_scales=torch.from_numpy(sa).to(device), b_scales=torch.from_numpy(sb).to(device),
+              output_dtype=torch.bfloat16)
+    first = gemm(*args, "int8", **kw)
+    for _ in range(3):
+        assert torch.equal(gemm(*args, "int8", **kw), first)

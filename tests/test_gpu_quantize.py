@@ -1,0 +1,112 @@
+"""GPU parity of the per-row quantizer (m5k_quantize_rows) against the CPU oracle.
+
+Bar: bit-exact codes and bit-exact FP32 scales (the reference itself demands exact codes,
+tests/test_metal.py:70-82 of the reference, scale rtol 1e-6; we hold scales exactly).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits_of, np_of
+from m5kernels_amd import quantize
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
+
+
+def _input(kind, shape, seed=41):
+    x = np.random.default_rng(seed).standard_normal(shape, dtype=np.float32)
+    if kind == "zeros":
+        x.fill(0)
+    elif kind == "outliers":
+        x[:, ::31] *= 30
+    return x
+
+
+def _check(xt, mode):
+    q, s = quantize(xt, mode)
+    torch.cuda.synchronize()
+    x32 = xt.float().cpu().numpy()  # exact decode of the stored input
+    rq, rs = ref.quantize_reference(x32, mode)
+    assert q.dtype == (torch.uint8 if mode == "fp8" else torch.int8)
+    np.testing.assert_array_equal(np_of(q), rq)
+    np.testing.assert_array_equal(np_of(s), rs)
+    return q, s
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+@pytest.mark.parametrize("kind", ["normal", "zeros", "outliers"])
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("shape", [(7, 256), (3, 5376), (5, 100), (2, 33), (4, 40000)])
+def test_quantizer_bit_exact(mode, kind, dtype, shape, device):
+    x = _input(kind, shape)
+    _check(torch.from_numpy(x).to(device).to(DTYPES[dtype]), mode)
+
+
+def test_config1_activation_bit_exact_vs_c_oracle(device):
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((256, 1024), dtype=np.float32)
+    at = torch.from_numpy(a).to(device).to(torch.bfloat16)
+    q, s = quantize(at, "int8")
+    rq, rs = ref.c_quantize_rows(bits_of(at), "int8")
+    np.testing.assert_array_equal(np_of(q), rq)
+    np.testing.assert_array_equal(np_of(s), rs)
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_ffn_down_activation_full_size_bit_exact(mode, device):
+    """BASELINE FFN-down activation [4096, 16384] bf16 with 0.1% x50 outlier channels."""
+    g = torch.Generator(device="cpu").manual_seed(29)
+    a = torch.randn((4096, 16384), generator=g, dtype=torch.float32)
+    a[:, ::1024] *= 50
+    at = a.to(device).to(torch.bfloat16)
+    q, s = quantize(at, mode)
+    rq, rs = ref.c_quantize_rows(bits_of(at), mode)
+    np.testing.assert_array_equal(np_of(s), rs)
+    np.testing.assert_array_equal(np_of(q), rq)
+
+
+def test_round_half_even_kat(kats, device):
+    kat = kats["int8_round_half_even"]
+    x = torch.tensor([kat["row"]] * 3, dtype=torch.float32, device=device)
+    q, s = quantize(x, "int8")
+    np.testing.assert_array_equal(np_of(q), np.tile(kat["codes"], (3, 1)))
+    np.testing.assert_array_equal(np_of(s), kat["scale"])
+
+
+def test_fp8_encoder_kat_and_all_codes(kats, device):
+    kat = kats["fp8_encode"]
+    # With the row peak at 448 the scale is exactly 1, so codes are fp8_encode(x) itself.
+    row = [v for v in kat["x"] if abs(v) <= 448]
+    codes = [c for v, c in zip(kat["x"], kat["codes"]) if abs(v) <= 448]
+    q, s = quantize(torch.tensor([row], dtype=torch.float32, device=device), "fp8")
+    assert float(s[0]) == 1.0
+    np.testing.assert_array_equal(np_of(q)[0], codes)
+    every = np.concatenate([np.arange(127), np.arange(128, 255)]).astype(np.uint8)
+    q, s = quantize(torch.from_numpy(ref.fp8_decode(every)[None, :]).to(device), "fp8")
+    assert float(s[0]) == 1.0
+    np.testing.assert_array_equal(np_of(q)[0], every)
+
+
+def test_fp8_ties_and_saturation(device):
+    table = ref.fp8_decode(np.arange(127, dtype=np.uint8)).astype(np.float64)
+    mids = ((table[:-1] + table[1:]) / 2).astype(np.float32)
+    row = np.concatenate([[448.0], mids, -mids, np.nextafter(mids, np.float32(0)), [447.99]]).astype(np.float32)
+    q, s = quantize(torch.from_numpy(row[None, :]).to(device), "fp8")
+    assert float(s[0]) == 1.0
+    np.testing.assert_array_equal(np_of(q)[0], ref.fp8_encode(row))
+
+
+def test_inputs_not_mutated_and_strided(device):
+    base = torch.randn(64, 512, device=device, dtype=torch.bfloat16)
+    view = base[:, ::2]
+    before = base.clone()
+    q, s = quantize(view, "int8")
+    rq, rs = ref.quantize_reference(view.float().cpu().numpy(), "int8")
+    np.testing.assert_array_equal(np_of(q), rq)
+    assert torch.equal(base, before)
