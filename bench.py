@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """W8A8 FFN-down on one MI355X, online activation quantization included.
 
-Workload (BASELINE.json metric and configs[2], FFN-down leg): A bf16 [4096, 16384] ~N(0,1)
+Workload (the headline metric: FFN-down of the FFN up/down configuration): A bf16 [4096, 16384] ~N(0,1)
 with 0.1% of channels (every 1024th) scaled x50, W bf16 [4096, 16384] ~N(0, 0.02), seed 29,
 synthetic.  Offline (untimed): W -> per-output-channel INT8 codes + FP32 scales.  One step
 = quantize(A) (per-token INT8) + W8A8 MFMA GEMM with the FP32 scale epilogue -> BF16 C.

@@ -135,6 +135,46 @@ int m5k_hadamard_rotate(const void* x, int x_dtype, int64_t rows, int64_t k, int
 int m5k_hadamard_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int block,
                                const int8_t* signs, int8_t* q, float* scales, void* stream);
 
+/*
+ * Fused row preparation (one dispatch): [gated residual update] -> RMS or LayerNorm ->
+ * modulation -> O cast -> signs -> block Hadamard -> per-row INT8.
+ * Replaces norm_hadamard.fused_norm_hadamard_quantize (branch == NULL) and
+ * fused_gated_residual_norm_hadamard_quantize (src/m5kernels/norm_hadamard.py:122-265,
+ * shaders/norm_hadamard.metal:1-121).
+ *   x: [rows,k] of x_dtype (the residual when gated); k % block == 0.
+ *   gated: branch [rows,k] (x_dtype), gate [k] or [P,k] with gate_row_map[rows];
+ *          residual_out[rows,k] (x_dtype) receives R(x + branch*gate), written once.
+ *   gamma [k]; scale/shift [k], or [P,k] tables selected by row_map[rows]; gamma, scale,
+ *   shift and gate share param_dtype (BF16 or F32).  signs int8 [k].
+ *   norm: M5K_NORM_RMS / M5K_NORM_LAYER; round_to_input: 1 rounds the modulated value to
+ *   x_dtype before the signs (round_output="input"), 0 keeps FP32.
+ *   Outputs: q int8 [rows,k], scales float32 [rows].
+ */
+int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t rows, int64_t k, const void* branch,
+                               const void* gate, const int32_t* gate_row_map, const void* gamma,
+                               const void* scale, const void* shift, int param_dtype,
+                               const int32_t* row_map, const int8_t* signs, int block, int norm,
+                               float epsilon, int round_to_input, int8_t* q, float* scales,
+                               void* residual_out, void* stream);
+
+/*
+ * Staged norm + modulation with the fused kernel's arithmetic and reduction tree.
+ * Replaces norm_hadamard.unfused_norm (src/m5kernels/norm_hadamard.py:321-348,
+ * shaders/norm_modulate.metal:1-37).  y: [rows,k] of x_dtype (round_to_input=1) or F32.
+ */
+int m5k_norm_modulate(const void* x, int x_dtype, int64_t rows, int64_t k, const void* gamma,
+                      const void* scale, const void* shift, int param_dtype, const int32_t* row_map,
+                      int norm, float epsilon, int round_to_input, void* y, void* stream);
+
+/*
+ * Staged gated residual update out = R(float(residual) + float(branch) * float(gate)).
+ * Replaces norm_hadamard.gated_residual_add (src/m5kernels/norm_hadamard.py:280-300,
+ * shaders/gated_residual.metal:1-9).  gate [k] or [P,k] with gate_row_map[rows].
+ */
+int m5k_gated_residual_add(const void* residual, int dtype, int64_t rows, int64_t k, const void* branch,
+                           const void* gate, int gate_dtype, const int32_t* gate_row_map, void* out,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

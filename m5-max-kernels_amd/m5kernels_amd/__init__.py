@@ -7,6 +7,12 @@ behind a C ABI (include/m5k.h).  There is no CPU fallback.
 
 from .hip import gemm, gemm_i8_accumulators, quantize
 from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
+from .norm_hadamard import (
+    fused_gated_residual_norm_hadamard_quantize,
+    fused_norm_hadamard_quantize,
+    gated_residual_add,
+    unfused_norm,
+)
 
 __all__ = [
     "quantize",
@@ -15,4 +21,8 @@ __all__ = [
     "rotate",
     "rotate_quantize",
     "SUPPORTED_BLOCK_SIZES",
+    "fused_norm_hadamard_quantize",
+    "fused_gated_residual_norm_hadamard_quantize",
+    "gated_residual_add",
+    "unfused_norm",
 ]

@@ -30,6 +30,7 @@ _DTYPE_CODES = {
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
+_f32 = ctypes.c_float
 
 # name -> argtypes (restype is int status unless noted)
 SIGNATURES = {
@@ -40,6 +41,11 @@ SIGNATURES = {
     "m5k_gemm_float": [_p, _p, _i32, _i64, _i64, _i64, _p, _i32, _p, _p, _p, _p],
     "m5k_hadamard_rotate": [_p, _i32, _i64, _i64, _i32, _p, _p, _p],
     "m5k_hadamard_quantize_rows": [_p, _i32, _i64, _i64, _i32, _p, _p, _p, _p],
+    "m5k_norm_hadamard_quantize": [
+        _p, _i32, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _p,
+    ],
+    "m5k_norm_modulate": [_p, _i32, _i64, _i64, _p, _p, _p, _i32, _p, _i32, _f32, _i32, _p, _p],
+    "m5k_gated_residual_add": [_p, _i32, _i64, _i64, _p, _p, _i32, _p, _p, _p],
 }
 
 _LIB = None

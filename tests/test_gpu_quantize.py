@@ -60,7 +60,7 @@ def test_config1_activation_bit_exact_vs_c_oracle(device):
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
 def test_ffn_down_activation_full_size_bit_exact(mode, device):
-    """BASELINE FFN-down activation [4096, 16384] bf16 with 0.1% x50 outlier channels."""
+    """FFN-down activation [4096, 16384] bf16 with 0.1% x50 outlier channels."""
     g = torch.Generator(device="cpu").manual_seed(29)
     a = torch.randn((4096, 16384), generator=g, dtype=torch.float32)
     a[:, ::1024] *= 50
