@@ -3,10 +3,10 @@
 //
 // Workgroup tile 256 x 256, 4 wave64 in a 2 x 2 grid, each wave owning a 128 x 128
 // sub-tile as 4 x 4 blocks of 32 x 32 MFMA accumulators (256 accumulator registers,
-// allocated by the compiler into AGPR/VGPR).  K advances 128 bytes per stage; a stage is
-// A[256 x 128 B] + B[256 x 128 B] = 64 KiB of LDS, double-buffered (128 KiB of the
-// 160 KiB per CU).  LDS rows are 128 B with the 16-byte chunk index XOR-swizzled by
-// (row & 7), so the 32 lanes reading one MFMA fragment column hit distinct banks.
+// allocated by the compiler into AGPRs).  K advances 64 bytes per stage; a stage is
+// A[256 x 64 B] + B[256 x 64 B] = 32 KiB of LDS in a ring of 4 stages (128 KiB of the
+// 160 KiB per CU), filled by direct global->LDS buffer loads issued 3 stages ahead.  LDS
+// rows are 64 B with the 16-byte chunk index XOR-swizzled by (row >> 2) & 3 (see swz()).
 //
 // MFMA operand layout (32 x 32 blocks): lane l supplies row (l & 31) and a 16-byte
 // (32-byte for FP8) slice of K selected by (l >> 5).  A and B use the same K-slice
@@ -14,6 +14,8 @@
 // (exact for INT32 accumulation).  Accumulator register r of lane l holds
 // C[(r >> 2) * 8 + (l >> 5) * 4 + (r & 3)][l & 31].
 #pragma once
+
+#include <type_traits>
 
 #include "m5k_common.h"
 
@@ -31,12 +33,27 @@ enum Mode { I8 = 0, F8 = 1, BF16 = 2, F16 = 3 };
 
 constexpr int BM = 256;   // tile rows (A rows / C rows)
 constexpr int BN = 256;   // tile cols (B rows / C cols)
-constexpr int BKB = 128;  // K bytes per stage
-constexpr int THREADS = 256;
-constexpr int WM = 128, WN = 128;  // wave sub-tile
-constexpr int FM = WM / 32, FN = WN / 32;
+constexpr int BKB = 64;   // K bytes per stage (LDS row length)
+constexpr int NST = 4;    // LDS stages in flight
 constexpr int STAGE_BYTES = BM * BKB;  // one operand, one stage
 constexpr int GROUP_M = 4;             // tile-rows per raster band
+
+// Wave grid of a 256 x 256 tile.  WAVES_M x WAVES_N wave64, each owning a (256/WAVES_M) x
+// (256/WAVES_N) sub-tile of 32 x 32 MFMA blocks.  2 x 2 = one wave per SIMD with 256
+// accumulator registers; 2 x 4 = two waves per SIMD with 128 each, so one wave's MFMAs keep
+// the pipe busy while its sibling waits at a barrier.
+template <int WAVES_M_, int WAVES_N_>
+struct Grid {
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int WAVES = WAVES_M * WAVES_N;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  static constexpr int FM = WM / 32, FN = WN / 32;
+  static constexpr int DMA_ROWS = BM / WAVES;      // rows of each operand one wave DMAs per stage
+  static constexpr int DMA_INSTR = DMA_ROWS / 16;  // 1 KiB (16 rows of 64 B) per instruction
+};
+using Grid4 = Grid<2, 2>;
+using Grid8 = Grid<2, 4>;
 
 template <int MODE>
 struct Traits {
@@ -105,132 +122,298 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tn = inner / h;
 }
 
-// Main loop.  ALIGNED: rows are 16-byte multiples and bases 16-byte aligned, so every
-// 16-byte chunk is either fully inside K or fully outside.  Otherwise bytes are loaded
-// one at a time with exact K bounds (small/odd shapes only).
-template <int MODE, bool ALIGNED>
-__device__ __forceinline__ void mainloop(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
-                                         int M, int N, int64_t Kb, int tile_m0, int tile_n0,
-                                         uint8_t* smem, typename Traits<MODE>::acc_t (&acc)[FM][FN]) {
-  using acc_t = typename Traits<MODE>::acc_t;
+// LDS layout of one operand stage: 256 rows x 64 bytes; the 16-byte chunk c of row r sits at
+// physical chunk c ^ ((r >> 2) & 3).  gfx950 serves ds_read_b128 16 lanes at a time over 64
+// banks (256 B); a fragment read covers 16 consecutive rows with one logical chunk, which
+// this swizzle spreads over all 16 bank groups (measured conflict-free on MI355X).
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+
+// Stage buffers are distinct __shared__ objects so the compiler can prove that fragment
+// reads of one stage never alias the direct-to-LDS loads filling another.
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_a0[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_a1[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_a2[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_a3[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_b0[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_b1[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_b2[STAGE_BYTES];
+__shared__ __attribute__((aligned(16))) uint8_t g_lds_b3[STAGE_BYTES];
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One 16-byte-per-lane buffer load straight into LDS: lane l's 16 bytes land at
+// lds_base + 16 l (M0 holds the wave-uniform LDS base); an offset past num_records loads 0.
+// Issued as inline asm so the compiler does not serialize it against LDS reads of other
+// stage buffers; every consumer waits with an explicit vmcnt and a barrier instead.  The
+// main loop issues no other vector-memory instruction, so those explicit counts are exact.
+__device__ __forceinline__ void dma16(uint32_t lds_base, uint32_t voffset, v4i rsrc) {
+  __asm__ volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds_base), "v"(voffset), "s"(rsrc)
+      : "memory", "m0");
+}
+
+__device__ __forceinline__ v4i buffer_rsrc(const void* base, uint32_t num_records) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  // word1: base[47:32], stride 0; word3: raw (untyped) 32-bit access, the gfx9 default.
+  return v4i{static_cast<int>(addr & 0xFFFFFFFFu), static_cast<int>((addr >> 32) & 0xFFFFu),
+             static_cast<int>(num_records), 0x00020000};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(const_cast<void*>(p))));
+}
+
+// Wait until at most N of this wave's DMA instructions are outstanding (vmcnt counts them
+// in issue order).
+template <int N>
+__device__ __forceinline__ void wait_stage() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence would wait for
+// every outstanding load of this wave, including the DMA of stages still being prefetched.
+// Callers wait explicitly (vmcnt for their own stage loads) before calling it.
+__device__ __forceinline__ void stage_barrier() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+template <int ST>
+__device__ __forceinline__ uint8_t* stage_a() {
+  return ST == 0 ? g_lds_a0 : ST == 1 ? g_lds_a1 : ST == 2 ? g_lds_a2 : g_lds_a3;
+}
+template <int ST>
+__device__ __forceinline__ uint8_t* stage_b() {
+  return ST == 0 ? g_lds_b0 : ST == 1 ? g_lds_b1 : ST == 2 ? g_lds_b2 : g_lds_b3;
+}
+
+// Fragments of one MFMA sub-step for a wave's FM x FN block grid.
+template <int MODE, class G>
+struct FragSet {
+  Frag<MODE> a[G::FM];
+  Frag<MODE> b[G::FN];
+};
+
+// Lane l reads row (l & 31) of each 32-row block; K slice: chunk 2s + (l >> 5) (16 bytes), or
+// chunks 2(l >> 5), +1 (32 bytes, FP8, one sub-step per stage).
+template <int MODE, class G>
+__device__ __forceinline__ void read_frags(const uint8_t* sa, const uint8_t* sb, int s, int a_row0, int b_row0,
+                                           int fhalf, int fsw, FragSet<MODE, G>& f) {
+  if constexpr (MODE == F8) {
+    const int c0 = fhalf * 2;
+    const int o0 = (c0 ^ fsw) << 4, o1 = ((c0 + 1) ^ fsw) << 4;
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i) {
+      const uint8_t* p = sa + (a_row0 + 32 * i) * BKB;
+      f.a[i].lo = *reinterpret_cast<const v4i*>(p + o0);
+      f.a[i].hi = *reinterpret_cast<const v4i*>(p + o1);
+    }
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) {
+      const uint8_t* p = sb + (b_row0 + 32 * j) * BKB;
+      f.b[j].lo = *reinterpret_cast<const v4i*>(p + o0);
+      f.b[j].hi = *reinterpret_cast<const v4i*>(p + o1);
+    }
+  } else {
+    const int o = ((s * 2 + fhalf) ^ fsw) << 4;
+#pragma unroll
+    for (int i = 0; i < G::FM; ++i) f.a[i].lo = *reinterpret_cast<const v4i*>(sa + (a_row0 + 32 * i) * BKB + o);
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) f.b[j].lo = *reinterpret_cast<const v4i*>(sb + (b_row0 + 32 * j) * BKB + o);
+  }
+}
+
+template <int MODE, class G>
+using AccTile = typename Traits<MODE>::acc_t[G::FM][G::FN];
+
+// MFMAs of block rows [I0, I1) of one fragment set.
+template <int MODE, class G, int I0, int I1>
+__device__ __forceinline__ void mfma_rows(AccTile<MODE, G>& acc, const FragSet<MODE, G>& f) {
+#pragma unroll
+  for (int i = I0; i < I1; ++i)
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) mfma<MODE>(acc[i][j], f.a[i], f.b[j]);
+}
+
+template <int MODE, class G>
+__device__ __forceinline__ void zero_acc(AccTile<MODE, G>& acc) {
+#pragma unroll
+  for (int i = 0; i < G::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) acc[i][j] = typename Traits<MODE>::acc_t{};
+}
+
+// Direct-to-LDS main loop (rows 16-byte multiples, bases 16-byte aligned, operands < 2 GiB).
+//
+// DMA: per stage each wave moves DMA_ROWS rows of both operand tiles with DMA_INSTR + DMA_INSTR
+// buffer loads of 1 KiB (lane l -> row 16i + l/4, physical chunk l & 3, i.e. logical chunk
+// (l & 3) ^ ((l >> 4) & 3)).  Rows past M/N and chunks past K read as zero through
+// out-of-range buffer offsets.  Stage k+3 is requested while stage k is computed.
+//
+// Per stage (one wave, I8/BF16/F16: two 32-byte sub-steps):
+//   read sub-step 1 fragments | MFMAs of sub-step 0
+//   wait for own stage k+1 loads; barrier   (stage k+1 visible; stage k-1 buffer free)
+//   DMA stage k+3 into the freed buffer
+//   read stage k+1 sub-step 0 fragments | MFMAs of sub-step 1
+// The barrier sits between the two MFMA groups, so its latency and the next stage's first
+// LDS reads overlap MFMAs already in flight.  FP8 (one 64-byte sub-step) splits its MFMAs
+// the same way by block rows and alternates the two fragment sets between stages.
+template <int MODE, class G>
+__device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int M,
+                                             int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc) {
+  constexpr int SUB = Traits<MODE>::sub_steps;
+  static_assert(SUB == 1 || SUB == 2, "stage holds one or two sub-steps");
+  constexpr int FM = G::FM;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  zero_acc<MODE, G>(acc);
 
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
+  const v4i rsrc_a = buffer_rsrc(A, static_cast<uint32_t>((int64_t)M * Kb));
+  const v4i rsrc_b = buffer_rsrc(B, static_cast<uint32_t>((int64_t)N * Kb));
+  constexpr uint32_t kOob = 0x80000000u;  // beyond num_records: the load returns zeros
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform copy for LDS bases
 
-  // Loader mapping: thread t moves chunk (t & 7) of rows (t >> 3) + 32 * i, i = 0..7.
-  const int lc = tid & 7, lr = tid >> 3;
-  const int sw_store = ((lr & 7) ^ lc) << 4;  // (row & 7) == (lr & 7) for every i
+  const int drow = wave * G::DMA_ROWS + (lane >> 2);  // row of DMA instruction 0
+  const int dchunk = (lane & 3) ^ ((lane >> 4) & 3);  // logical chunk (same for every i)
   const int64_t kt_count = (Kb + BKB - 1) / BKB;
+  const int64_t kt_padded = (kt_count + NST - 1) / NST * NST;
 
-  uint4 ra[8], rb[8];
-  auto gload = [&](int64_t kt) {
-    const int64_t kb = kt * BKB + lc * 16;
+  // Per-lane source offsets of each DMA instruction (kOob for rows past M / N).
+  uint32_t a_base[G::DMA_INSTR], b_base[G::DMA_INSTR];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = lr + 32 * i;
-      const int am = tile_m0 + r, bn = tile_n0 + r;
-      if constexpr (ALIGNED) {
-        ra[i] = (am < M && kb < Kb) ? *reinterpret_cast<const uint4*>(A + (int64_t)am * Kb + kb)
-                                    : make_uint4(0, 0, 0, 0);
-        rb[i] = (bn < N && kb < Kb) ? *reinterpret_cast<const uint4*>(B + (int64_t)bn * Kb + kb)
-                                    : make_uint4(0, 0, 0, 0);
-      } else {
-        uint32_t wa[4] = {0, 0, 0, 0}, wb[4] = {0, 0, 0, 0};
+  for (int i = 0; i < G::DMA_INSTR; ++i) {
+    const int r = drow + 16 * i;
+    a_base[i] = tile_m0 + r < M ? static_cast<uint32_t>((int64_t)(tile_m0 + r) * Kb + dchunk * 16) : kOob;
+    b_base[i] = tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb + dchunk * 16) : kOob;
+  }
+  const uint32_t lds_row0 = static_cast<uint32_t>(uwave * G::DMA_ROWS * BKB);
+  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kt) {
+    const uint32_t kofs = static_cast<uint32_t>(kt * BKB);
+    const bool kin = static_cast<int64_t>(kofs) + dchunk * 16 < Kb;
+    const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const bool kin = kb + e < Kb;
-          const uint32_t va = (am < M && kin) ? A[(int64_t)am * Kb + kb + e] : 0u;
-          const uint32_t vb = (bn < N && kin) ? B[(int64_t)bn * Kb + kb + e] : 0u;
-          wa[e >> 2] |= va << (8 * (e & 3));
-          wb[e >> 2] |= vb << (8 * (e & 3));
-        }
-        ra[i] = make_uint4(wa[0], wa[1], wa[2], wa[3]);
-        rb[i] = make_uint4(wb[0], wb[1], wb[2], wb[3]);
-      }
-    }
-  };
-  auto sstore = [&](int stage) {
-    uint8_t* sa = smem + stage * 2 * STAGE_BYTES;
-    uint8_t* sb = sa + STAGE_BYTES;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int off = (lr + 32 * i) * BKB + sw_store;
-      *reinterpret_cast<uint4*>(sa + off) = ra[i];
-      *reinterpret_cast<uint4*>(sb + off) = rb[i];
+    for (int i = 0; i < G::DMA_INSTR; ++i) {
+      dma16(la + 16 * i * BKB, (kin && a_base[i] != kOob) ? a_base[i] + kofs : kOob, rsrc_a);
+      dma16(lb + 16 * i * BKB, (kin && b_base[i] != kOob) ? b_base[i] + kofs : kOob, rsrc_b);
     }
   };
 
-  // Fragment addressing: row (lane & 31) of each 32-row block; swizzle uses row & 7 == lane & 7.
-  const int frow = lane & 31, fhalf = lane >> 5, fsw = lane & 7;
-  const int a_row0 = wm * WM + frow, b_row0 = wn * WN + frow;
+  const int frow = lane & 31, fhalf = lane >> 5, fsw = swz(frow);
+  const int a_row0 = wm * G::WM + frow, b_row0 = wn * G::WN + frow;
 
-  auto compute = [&](int stage) {
-    const uint8_t* sa = smem + stage * 2 * STAGE_BYTES;
-    const uint8_t* sb = sa + STAGE_BYTES;
-#pragma unroll
-    for (int s = 0; s < Traits<MODE>::sub_steps; ++s) {
-      Frag<MODE> fa[FM], fb[FN];
-      if constexpr (MODE == F8) {
-        const int c0 = s * 4 + fhalf * 2;
-        const int o0 = ((c0 ^ fsw) << 4), o1 = (((c0 + 1) ^ fsw) << 4);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          const uint8_t* p = sa + (a_row0 + 32 * i) * BKB;
-          fa[i].lo = *reinterpret_cast<const v4i*>(p + o0);
-          fa[i].hi = *reinterpret_cast<const v4i*>(p + o1);
-        }
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const uint8_t* p = sb + (b_row0 + 32 * j) * BKB;
-          fb[j].lo = *reinterpret_cast<const v4i*>(p + o0);
-          fb[j].hi = *reinterpret_cast<const v4i*>(p + o1);
-        }
-      } else {
-        const int o = (((s * 2 + fhalf) ^ fsw) << 4);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i].lo = *reinterpret_cast<const v4i*>(sa + (a_row0 + 32 * i) * BKB + o);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) fb[j].lo = *reinterpret_cast<const v4i*>(sb + (b_row0 + 32 * j) * BKB + o);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) mfma<MODE>(acc[i][j], fa[i], fb[j]);
+  FragSet<MODE, G> f0, f1;
+
+  // One stage: buffer CUR, DMA target FREE (= stage k+3), next buffer NXT.  For FP8 the
+  // current fragments live in f0 on even stages and f1 on odd ones (P selects).
+  auto stage = [&](auto cur_tag, auto nxt_tag, auto free_tag, auto parity_tag, int64_t kt) {
+    constexpr int CUR = decltype(cur_tag)::value, NXT = decltype(nxt_tag)::value;
+    constexpr int FREE = decltype(free_tag)::value, P = decltype(parity_tag)::value;
+    if constexpr (SUB == 2) {
+      read_frags<MODE, G>(stage_a<CUR>(), stage_b<CUR>(), 1, a_row0, b_row0, fhalf, fsw, f1);
+      mfma_rows<MODE, G, 0, FM>(acc, f0);
+      wait_stage<2 * G::DMA_INSTR>();
+      stage_barrier();
+      dma(stage_a<FREE>(), stage_b<FREE>(), kt + 3);
+      read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fhalf, fsw, f0);
+      mfma_rows<MODE, G, 0, FM>(acc, f1);
+    } else {
+      FragSet<MODE, G>& fc = P ? f1 : f0;
+      FragSet<MODE, G>& fn = P ? f0 : f1;
+      mfma_rows<MODE, G, 0, FM / 2>(acc, fc);
+      wait_stage<2 * G::DMA_INSTR>();
+      stage_barrier();
+      dma(stage_a<FREE>(), stage_b<FREE>(), kt + 3);
+      read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fhalf, fsw, fn);
+      mfma_rows<MODE, G, FM / 2, FM>(acc, fc);
     }
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  dma(stage_a<0>(), stage_b<0>(), 0);
+  dma(stage_a<1>(), stage_b<1>(), 1);
+  dma(stage_a<2>(), stage_b<2>(), 2);
+  wait_stage<4 * G::DMA_INSTR>();  // stage 0 landed (own loads)
+  stage_barrier();
+  read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fhalf, fsw, f0);
+  for (int64_t kt = 0; kt < kt_padded; kt += NST) {
+    stage(I0{}, I1{}, I3{}, I0{}, kt);
+    stage(I1{}, I2{}, I0{}, I1{}, kt + 1);
+    stage(I2{}, I3{}, I1{}, I0{}, kt + 2);
+    stage(I3{}, I0{}, I2{}, I1{}, kt + 3);
+  }
+  // Drain the trailing (zero) DMAs before the LDS is reused or the wave exits.
+  wait_stage<0>();
+  stage_barrier();
+}
+
+// Register-staged main loop for rows that are not 16-byte multiples (small, odd K): bytes
+// are loaded one at a time with exact bounds, then stored to the same swizzled layout.
+template <int MODE, class G>
+__device__ __forceinline__ void mainloop_staged(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int M,
+                                                int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc) {
+  constexpr int SUB = Traits<MODE>::sub_steps;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  zero_acc<MODE, G>(acc);
+  constexpr int ROWS_PER_PASS = G::THREADS / 4;  // chunk (t & 3) of rows (t >> 2) + pass * ROWS_PER_PASS
+  const int lc = tid & 3, lr = tid >> 2;
+  const int64_t kt_count = (Kb + BKB - 1) / BKB;
+  const int frow = lane & 31, fhalf = lane >> 5, fsw = swz(frow);
+  const int a_row0 = wm * G::WM + frow, b_row0 = wn * G::WN + frow;
   for (int64_t kt = 0; kt < kt_count; ++kt) {
-    const bool more = kt + 1 < kt_count;
-    if (more) gload(kt + 1);
-    compute(static_cast<int>(kt & 1));
-    if (more) sstore(static_cast<int>((kt + 1) & 1));
+    const int64_t kb = kt * BKB + lc * 16;
+    for (int i = 0; i < BM / ROWS_PER_PASS; ++i) {
+      const int r = lr + ROWS_PER_PASS * i;
+      const int am = tile_m0 + r, bn = tile_n0 + r;
+      uint32_t wa[4] = {0, 0, 0, 0}, wb[4] = {0, 0, 0, 0};
+      for (int e = 0; e < 16; ++e) {
+        const bool kin = kb + e < Kb;
+        const uint32_t va = (am < M && kin) ? A[(int64_t)am * Kb + kb + e] : 0u;
+        const uint32_t vb = (bn < N && kin) ? B[(int64_t)bn * Kb + kb + e] : 0u;
+        wa[e >> 2] |= va << (8 * (e & 3));
+        wb[e >> 2] |= vb << (8 * (e & 3));
+      }
+      const int off = r * BKB + ((lc ^ swz(r)) << 4);
+      *reinterpret_cast<uint4*>(g_lds_a0 + off) = make_uint4(wa[0], wa[1], wa[2], wa[3]);
+      *reinterpret_cast<uint4*>(g_lds_b0 + off) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < SUB; ++s) {
+      FragSet<MODE, G> f;
+      read_frags<MODE, G>(g_lds_a0, g_lds_b0, s, a_row0, b_row0, fhalf, fsw, f);
+      mfma_rows<MODE, G, 0, G::FM>(acc, f);
+    }
     __syncthreads();
   }
 }
 
 // Visit every accumulator element with its global (row, col).
-template <class AccT, class F>
-__device__ __forceinline__ void for_each_acc(const AccT (&acc)[FM][FN], int tile_m0, int tile_n0, F&& f) {
+template <class G, class AccT, class F>
+__device__ __forceinline__ void for_each_acc(const AccT (&acc)[G::FM][G::FN], int tile_m0, int tile_n0, F&& f) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
   const int col_in = lane & 31, row_half = (lane >> 5) * 4;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < G::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < G::FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = tile_m0 + wm * WM + i * 32 + (r >> 2) * 8 + row_half + (r & 3);
-        const int n = tile_n0 + wn * WN + j * 32 + col_in;
+        const int m = tile_m0 + wm * G::WM + i * 32 + (r >> 2) * 8 + row_half + (r & 3);
+        const int n = tile_n0 + wn * G::WN + j * 32 + col_in;
         f(m, n, acc[i][j][r]);
       }
 }

@@ -29,20 +29,23 @@ struct EpiParams {
 };
 
 // RAW: write INT32 accumulators (I8 only).
+// Wave grid used by every GEMM kernel of the library.
+using KernelGrid = Grid8;
+
 template <int MODE, bool ALIGNED, int OUT_DT, int BIAS, int GATE, bool RAW>
-__global__ __launch_bounds__(THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
-                                                          const uint8_t* __restrict__ B, int M, int N,
-                                                          int64_t Kb, EpiParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * STAGE_BYTES];
-  using acc_t = typename Traits<MODE>::acc_t;
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
+                                                                      const uint8_t* __restrict__ B, int M, int N,
+                                                                      int64_t Kb, EpiParams p) {
+  using G = KernelGrid;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  acc_t acc[FM][FN];
-  mainloop<MODE, ALIGNED>(A, B, M, N, Kb, m0, n0, smem, acc);
+  AccTile<MODE, G> acc;
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+  else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
 
-  for_each_acc(acc, m0, n0, [&](int m, int n, auto v) {
+  for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
     if (m >= M || n >= N) return;
     const int64_t idx = (int64_t)m * N + n;
     if constexpr (RAW) {
@@ -74,8 +77,10 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   const int64_t kb = k * Traits<MODE>::elem_bytes;
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
   M5K_REQUIRE(tiles <= 0x7FFFFFFF, "%s: too many tiles", name);
-  const bool aligned = kb % 16 == 0 && aligned16(a) && aligned16(b);
-  const dim3 grid(static_cast<unsigned>(tiles)), block(THREADS);
+  // The direct-to-LDS path addresses each operand through a 32-bit buffer descriptor.
+  const bool aligned = kb % 16 == 0 && aligned16(a) && aligned16(b) && m * kb < (int64_t(1) << 31) &&
+                       n * kb < (int64_t(1) << 31);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(KernelGrid::THREADS);
   auto* A = static_cast<const uint8_t*>(a);
   auto* B = static_cast<const uint8_t*>(b);
   if (aligned)
