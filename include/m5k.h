@@ -175,6 +175,27 @@ int m5k_gated_residual_add(const void* residual, int dtype, int64_t rows, int64_
                            const void* gate, int gate_dtype, const int32_t* gate_row_map, void* out,
                            void* stream);
 
+/*
+ * Q or K projection + per-head RMSNorm + split-half RoPE, head-major BF16 output.
+ * Replaces qk_rope.projection_qk_rope (src/m5kernels/qk_rope.py:120-182,
+ * shaders/qk_rope_projection.metal:1-39, shaders/qk_rope_body.metal:1-20).
+ *   a [m,k], b [n,k] of ab_dtype: M5K_I8 (with float32 a_scales[m], b_scales[n]; k <= 131071)
+ *   or M5K_BF16 (scales NULL); n % 128 == 0.  gamma bf16 [128]; cos, sin bf16 [m, rope_half],
+ *   0 <= rope_half <= 64.  y bf16 [n/128, m, 128].
+ *   z = bf16(projection); inv = 1/sqrt(sum(z^2)/128 + eps); u = z*inv*gamma;
+ *   y[d] = u[d]*c - u[d+R]*s (d < R), u[d]*c + u[d-R]*s (R <= d < 2R), u[d] otherwise.
+ */
+int m5k_projection_qk_rope(const void* a, const void* b, int ab_dtype, int64_t m, int64_t n, int64_t k,
+                           const float* a_scales, const float* b_scales, const void* gamma, const void* cos,
+                           const void* sin, int rope_half, float epsilon, void* y, void* stream);
+
+/*
+ * Staged postprocess of a BF16 [m,n] projection with the fused kernel's per-(row, head) code.
+ * Replaces qk_rope.qk_norm_rope (src/m5kernels/qk_rope.py:185-203, shaders/qk_rope_norm.metal).
+ */
+int m5k_qk_norm_rope(const void* projected, int64_t m, int64_t n, const void* gamma, const void* cos,
+                     const void* sin, int rope_half, float epsilon, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

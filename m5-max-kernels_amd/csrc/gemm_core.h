@@ -128,16 +128,12 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 // this swizzle spreads over all 16 bank groups (measured conflict-free on MI355X).
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
-// Stage buffers are distinct __shared__ objects so the compiler can prove that fragment
-// reads of one stage never alias the direct-to-LDS loads filling another.
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_a0[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_a1[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_a2[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_a3[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_b0[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_b1[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_b2[STAGE_BYTES];
-__shared__ __attribute__((aligned(16))) uint8_t g_lds_b3[STAGE_BYTES];
+// All LDS of a GEMM kernel: NST stages x (A, B) x 16 KiB = 128 KiB.  The main loop uses it as
+// the stage ring; epilogues may reuse it afterwards (e.g. as a 256 x 256 BF16 tile).  The DMA
+// writes are inline asm with "memory" clobbers and every consumer sits behind an explicit
+// wait and barrier, so one array serves all stages.
+constexpr int LDS_BYTES = NST * 2 * STAGE_BYTES;
+__shared__ __attribute__((aligned(16))) uint8_t g_lds[LDS_BYTES];
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -186,11 +182,11 @@ __device__ __forceinline__ void stage_barrier() {
 
 template <int ST>
 __device__ __forceinline__ uint8_t* stage_a() {
-  return ST == 0 ? g_lds_a0 : ST == 1 ? g_lds_a1 : ST == 2 ? g_lds_a2 : g_lds_a3;
+  return g_lds + ST * 2 * STAGE_BYTES;
 }
 template <int ST>
 __device__ __forceinline__ uint8_t* stage_b() {
-  return ST == 0 ? g_lds_b0 : ST == 1 ? g_lds_b1 : ST == 2 ? g_lds_b2 : g_lds_b3;
+  return g_lds + ST * 2 * STAGE_BYTES + STAGE_BYTES;
 }
 
 // Fragments of one MFMA sub-step for a wave's FM x FN block grid.
@@ -385,14 +381,14 @@ __device__ __forceinline__ void mainloop_staged(const uint8_t* __restrict__ A, c
         wb[e >> 2] |= vb << (8 * (e & 3));
       }
       const int off = r * BKB + ((lc ^ swz(r)) << 4);
-      *reinterpret_cast<uint4*>(g_lds_a0 + off) = make_uint4(wa[0], wa[1], wa[2], wa[3]);
-      *reinterpret_cast<uint4*>(g_lds_b0 + off) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+      *reinterpret_cast<uint4*>(stage_a<0>() + off) = make_uint4(wa[0], wa[1], wa[2], wa[3]);
+      *reinterpret_cast<uint4*>(stage_b<0>() + off) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
     }
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < SUB; ++s) {
       FragSet<MODE, G> f;
-      read_frags<MODE, G>(g_lds_a0, g_lds_b0, s, a_row0, b_row0, fhalf, fsw, f);
+      read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), s, a_row0, b_row0, fhalf, fsw, f);
       mfma_rows<MODE, G, 0, G::FM>(acc, f);
     }
     __syncthreads();

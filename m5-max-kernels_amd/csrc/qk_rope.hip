@@ -1,0 +1,212 @@
+// Q/K projection + per-head RMSNorm + split-half RoPE with head-major BF16 output.
+//
+// Contract: qk_rope.py:120-203 with the arithmetic of shaders/qk_rope_projection.metal:26-33
+// and shaders/qk_rope_body.metal:1-20.  For one row m and head h (128 channels):
+//   z[d]  = bf16(projection)            INT8: bf16((float(acc) * sa[m]) * sb[n]);  BF16: bf16(acc)
+//   inv   = 1 / sqrt(sum_d z[d]^2 / 128 + eps)
+//   u[d]  = (z[d] * inv) * gamma[d]
+//   d < R:      y[d] = u[d] * c[j] - u[d+R] * s[j]      (j = d)
+//   R <= d < 2R: y[d] = u[d] * c[j] + u[d-R] * s[j]     (j = d - R)
+//   d >= 2R:    y[d] = u[d]
+//   Y[h, m, d] = bf16(y[d]);  c, s = cos/sin[m, j] (bf16)
+// Every product and sum is a separate FP32 operation (the library is built without FMA
+// contraction).
+//
+// The fused kernel runs the GEMM main loop for a 256-row x 2-head tile, stages the BF16
+// projection in the (then free) 128 KiB of LDS, and normalizes each (row, head) with a group
+// of 16 lanes (8 channels each, one 16-byte read and one 16-byte head-major store per lane).
+// The staged kernel runs the same per-(row, head) routine on a BF16 [M,N] projection in HBM,
+// so the two paths agree bit for bit whenever their projections do.
+#include "gemm_launch.h"
+
+namespace m5k {
+namespace qk {
+namespace {
+
+using namespace m5k::gemm;
+using m5k::gemm::detail::KernelGrid;
+
+constexpr int HEAD = 128;
+
+struct QkParams {
+  const uint16_t* gamma;  // bf16 [128]
+  const uint16_t* cos;    // bf16 [M, R]
+  const uint16_t* sin;    // bf16 [M, R]
+  int rope_half;          // R in [0, 64]
+  float eps;
+  uint16_t* y;            // bf16 [N/128, M, 128]
+};
+
+// Normalize + rotate one (row, head).  lg in [0,16) owns channels [8 lg, 8 lg + 8); z holds
+// them; partner(d) returns channel d of the same (row, head).  All 16 lanes of the group must
+// call together (width-16 exchanges).
+template <class Partner>
+__device__ __forceinline__ void norm_rope_16(const float (&z)[8], Partner partner, const QkParams& p, int64_t row,
+                                             int64_t m_rows, int head, int lg) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ss += z[t] * z[t];
+  ss += __shfl_xor(ss, 1, 16);
+  ss += __shfl_xor(ss, 2, 16);
+  ss += __shfl_xor(ss, 4, 16);
+  ss += __shfl_xor(ss, 8, 16);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(HEAD) + p.eps);
+  const int R = p.rope_half;
+  const uint16_t* crow = p.cos + row * R;
+  const uint16_t* srow = p.sin + row * R;
+  uint32_t packed[4];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int d = 8 * lg + t;
+    float v = (z[t] * inv) * bf16_bits_to_f32(p.gamma[d]);
+    if (d < 2 * R) {
+      const bool lower = d < R;
+      const int pair = lower ? d + R : d - R;
+      const int j = lower ? d : d - R;
+      const float pv = (partner(pair) * inv) * bf16_bits_to_f32(p.gamma[pair]);
+      const float c = bf16_bits_to_f32(crow[j]), s = bf16_bits_to_f32(srow[j]);
+      v = lower ? (v * c) - (pv * s) : (v * c) + (pv * s);
+    }
+    const uint32_t bits = f32_to_bf16_bits(v);
+    if (t & 1) packed[t >> 1] |= bits << 16;
+    else packed[t >> 1] = bits;
+  }
+  uint16_t* out = p.y + (static_cast<int64_t>(head) * m_rows + row) * HEAD + 8 * lg;
+  *reinterpret_cast<uint4*>(out) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+}
+
+template <int MODE, bool ALIGNED>
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const uint8_t* __restrict__ A,
+                                                                          const uint8_t* __restrict__ B, int M, int N,
+                                                                          int64_t Kb, const float* __restrict__ sa,
+                                                                          const float* __restrict__ sb, QkParams p) {
+  using G = KernelGrid;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  AccTile<MODE, G> acc;
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+  else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+
+  // BF16 projection tile [256 rows][256 cols] in LDS (row stride 512 B).  The main loop ended
+  // with a drained DMA and a barrier, so the stage ring is free.
+  uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
+  for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
+    float value;
+    if constexpr (MODE == I8) value = (m < M && n < N) ? (static_cast<float>(v) * sa[m]) * sb[n] : 0.0f;
+    else value = v;
+    tile[(m - m0) * BN + (n - n0)] = static_cast<uint16_t>(f32_to_bf16_bits(value));
+  });
+  __syncthreads();
+
+  const int group = threadIdx.x >> 4, lg = threadIdx.x & 15;
+  constexpr int GROUPS = G::THREADS / 16;
+  for (int q = group; q < BM * 2; q += GROUPS) {
+    const int local_row = q >> 1, local_head = q & 1;
+    const int row = m0 + local_row;
+    const int head = n0 / HEAD + local_head;
+    if (row >= M || head * HEAD >= N) continue;  // uniform across the 16-lane group
+    const uint16_t* src = tile + local_row * BN + local_head * HEAD;
+    const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float z[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      z[2 * t] = bf16_bits_to_f32(ws[t] & 0xFFFFu);
+      z[2 * t + 1] = bf16_bits_to_f32(ws[t] >> 16);
+    }
+    norm_rope_16(z, [&](int d) { return bf16_bits_to_f32(src[d]); }, p, row, M, head, lg);
+  }
+}
+
+// Staged postprocess of a BF16 [M, N] projection: one 16-lane group per (row, head), consecutive
+// groups walking the heads of a row (coalesced 256-byte reads).
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __restrict__ P, int64_t M, int64_t N,
+                                                           QkParams p) {
+  const int64_t heads = N / HEAD;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int lg = threadIdx.x & 15;
+  if (q >= M * heads) return;  // whole 16-lane groups leave together
+  const int64_t row = q / heads;
+  const int head = static_cast<int>(q - row * heads);
+  const uint16_t* src = P + row * N + static_cast<int64_t>(head) * HEAD;
+  const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  float z[8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    z[2 * t] = bf16_bits_to_f32(ws[t] & 0xFFFFu);
+    z[2 * t + 1] = bf16_bits_to_f32(ws[t] >> 16);
+  }
+  norm_rope_16(z, [&](int d) { return bf16_bits_to_f32(src[d]); }, p, row, M, head, lg);
+}
+
+template <int MODE>
+int launch_fused(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const float* sa, const float* sb,
+                 const QkParams& p, hipStream_t st) {
+  const int64_t kb = k * Traits<MODE>::elem_bytes;
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  const bool aligned = kb % 16 == 0 && aligned16(a) && aligned16(b) && m * kb < (int64_t(1) << 31) &&
+                       n * kb < (int64_t(1) << 31);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(KernelGrid::THREADS);
+  auto* A = static_cast<const uint8_t*>(a);
+  auto* B = static_cast<const uint8_t*>(b);
+  if (aligned) qk_fused_kernel<MODE, true><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p);
+  else qk_fused_kernel<MODE, false><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p);
+  return launch_status("m5k_projection_qk_rope");
+}
+
+int check_norm_args(int64_t m, int64_t n, const void* gamma, const void* cos, const void* sin, int rope_half,
+                    float epsilon, const void* y, const char* name) {
+  M5K_REQUIRE(m > 0 && n > 0 && n % HEAD == 0, "%s: need M > 0 and N a positive multiple of 128", name);
+  M5K_REQUIRE(m <= 0x7FFFFFFF && n <= 0x7FFFFFFF, "%s: M or N exceeds int32", name);
+  M5K_REQUIRE(gamma && y && (rope_half == 0 || (cos && sin)), "%s: null pointer", name);
+  M5K_REQUIRE(rope_half >= 0 && rope_half <= HEAD / 2, "%s: rope_half %d not in [0, 64]", name, rope_half);
+  M5K_REQUIRE(epsilon > 0.0f, "%s: epsilon must be positive", name);
+  M5K_REQUIRE(aligned16(y), "%s: y must be 16-byte aligned", name);
+  return M5K_OK;
+}
+
+}  // namespace
+}  // namespace qk
+}  // namespace m5k
+
+using namespace m5k;
+using namespace m5k::qk;
+
+extern "C" int m5k_projection_qk_rope(const void* a, const void* b, int ab_dtype, int64_t m, int64_t n, int64_t k,
+                                      const float* a_scales, const float* b_scales, const void* gamma,
+                                      const void* cos, const void* sin, int rope_half, float epsilon, void* y,
+                                      void* stream) {
+  clear_error();
+  const char* name = "m5k_projection_qk_rope";
+  if (int rc = check_norm_args(m, n, gamma, cos, sin, rope_half, epsilon, y, name)) return rc;
+  M5K_REQUIRE(a && b && k > 0, "%s: null operand or empty K", name);
+  QkParams p{static_cast<const uint16_t*>(gamma), static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+             rope_half, epsilon, static_cast<uint16_t*>(y)};
+  hipStream_t st = as_stream(stream);
+  if (ab_dtype == M5K_I8) {
+    M5K_REQUIRE(a_scales && b_scales, "%s: INT8 needs a_scales and b_scales", name);
+    M5K_REQUIRE(k <= 131071, "%s: K exceeds the INT32 worst-case bound 131071", name);
+    return launch_fused<I8>(a, b, m, n, k, a_scales, b_scales, p, st);
+  }
+  M5K_REQUIRE(ab_dtype == M5K_BF16, "%s: operands must be INT8 or BF16", name);
+  return launch_fused<BF16>(a, b, m, n, k, nullptr, nullptr, p, st);
+}
+
+extern "C" int m5k_qk_norm_rope(const void* projected, int64_t m, int64_t n, const void* gamma, const void* cos,
+                                const void* sin, int rope_half, float epsilon, void* y, void* stream) {
+  clear_error();
+  const char* name = "m5k_qk_norm_rope";
+  if (int rc = check_norm_args(m, n, gamma, cos, sin, rope_half, epsilon, y, name)) return rc;
+  M5K_REQUIRE(projected && aligned16(projected), "%s: projection must be a 16-byte aligned pointer", name);
+  QkParams p{static_cast<const uint16_t*>(gamma), static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+             rope_half, epsilon, static_cast<uint16_t*>(y)};
+  const int64_t groups = m * (n / HEAD);
+  const int64_t blocks = (groups + 15) / 16;
+  M5K_REQUIRE(blocks <= 0x7FFFFFFF, "%s: input too large", name);
+  qk_norm_rope_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream)>>>(
+      static_cast<const uint16_t*>(projected), m, n, p);
+  return launch_status(name);
+}

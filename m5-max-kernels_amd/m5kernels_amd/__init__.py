@@ -6,6 +6,7 @@ behind a C ABI (include/m5k.h).  There is no CPU fallback.
 """
 
 from .hip import gemm, gemm_i8_accumulators, quantize
+from .qk_rope import projection_qk_rope, qk_norm_rope
 from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
 from .norm_hadamard import (
     fused_gated_residual_norm_hadamard_quantize,
@@ -25,4 +26,6 @@ __all__ = [
     "fused_gated_residual_norm_hadamard_quantize",
     "gated_residual_add",
     "unfused_norm",
+    "projection_qk_rope",
+    "qk_norm_rope",
 ]

@@ -1,0 +1,216 @@
+"""GPU parity of the fused Q/K projection + RMSNorm + RoPE (m5k_projection_qk_rope) and the
+staged postprocess (m5k_qk_norm_rope).
+
+Bars: INT8 fused == staged (quantize -> gemm bf16 -> qk_norm_rope) bit for bit, as the reference
+requires (tests/test_qk_rope_metal.py:78-81 of the reference), and here also for BF16 since both
+paths share one main loop; both within rel-L2 1e-3 of the float64 reference fed the exact
+projection (the north-star RoPE bar; the reference's own gate is 0.008).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits_of, np_of
+from m5kernels_amd import gemm, projection_qk_rope, qk_norm_rope, quantize
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32(t):
+    return t.float().cpu().numpy()
+
+
+def _tables(rng, m, device, rope_half=48):
+    gamma = torch.from_numpy(rng.uniform(-1.5, 1.5, 128).astype(np.float32)).to(device).to(torch.bfloat16)
+    angles = rng.uniform(-4, 4, (m, rope_half)).astype(np.float32)
+    cos = torch.from_numpy(np.cos(angles)).to(device).to(torch.bfloat16)
+    sin = torch.from_numpy(np.sin(angles)).to(device).to(torch.bfloat16)
+    return gamma, cos, sin
+
+
+def _check(actual, expected, tol=1e-3):
+    assert actual.dtype == torch.bfloat16
+    got = _f32(actual)
+    assert np.isfinite(got).all()
+    assert ref.metrics(got, expected)["relative_l2"] < tol
+
+
+def _projection(a, b, mode, sa=None, sb=None):
+    """Exact projection: INT32 dot then the FP32 dequant order (float64 for BF16)."""
+    if mode == "int8":
+        dot = np_of(a).astype(np.int64) @ np_of(b).astype(np.int64).T
+        return (dot.astype(np.float32) * np_of(sa)[:, None]) * np_of(sb)[None, :]
+    return _f32(a).astype(np.float64) @ _f32(b).astype(np.float64).T
+
+
+@pytest.mark.parametrize("mode", ["int8", "bf16"])
+@pytest.mark.parametrize(
+    "shape,tile",
+    [
+        ((1, 128, 33), (16, 128, 4, 1)),
+        ((17, 384, 96), (32, 128, 4, 8)),
+        ((65, 256, 257), (64, 128, 8, 1)),
+        ((129, 128, 33), (128, 128, 4, 8)),
+        ((1, 128, 5376), (128, 64, 8, 8)),
+        ((300, 640, 1024), (64, 128, 4, 8)),
+        ((7, 128, 16), (16, 128, 8, 1)),
+    ],
+)
+def test_fused_projection_tiles_tails_and_reference(mode, shape, tile, device):
+    rng = np.random.default_rng(117)
+    m, n, k = shape
+    a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(torch.bfloat16)
+    b = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device).to(torch.bfloat16)
+    gamma, cos, sin = _tables(rng, m, device)
+    scales = {}
+    if mode == "int8":
+        a, sa = quantize(a, "int8")
+        b, sb = quantize(b, "int8")
+        scales = dict(a_scales=sa, b_scales=sb)
+    projected = _projection(a, b, mode, scales.get("a_scales"), scales.get("b_scales"))
+    expected = ref.qk_rope_reference(projected.reshape(m, n // 128, 128), _f32(gamma), _f32(cos), _f32(sin))["output"]
+    fused = projection_qk_rope(a, b, gamma, cos, sin, mode, tile, **scales)
+    staged = qk_norm_rope(gemm(a, b, mode, tile, output_dtype=torch.bfloat16, **scales), gamma, cos, sin)
+    assert fused.shape == staged.shape == (n // 128, m, 128)
+    _check(fused, expected)
+    _check(staged, expected)
+    np.testing.assert_array_equal(bits_of(fused), bits_of(staged))
+
+
+@pytest.mark.parametrize("mode", ["int8", "bf16"])
+@pytest.mark.parametrize("kind", ["zeros", "outliers"])
+def test_zeros_outliers_and_input_immutability(mode, kind, device):
+    rng = np.random.default_rng(33)
+    a_np = rng.standard_normal((7, 257), dtype=np.float32)
+    b_np = rng.standard_normal((384, 257), dtype=np.float32)
+    if kind == "zeros":
+        a_np.fill(0)
+        b_np.fill(0)
+    else:
+        a_np[:, ::31] *= 100
+        b_np[:, ::17] *= 100
+    a = torch.from_numpy(a_np).to(device).to(torch.bfloat16)
+    b = torch.from_numpy(b_np).to(device).to(torch.bfloat16)
+    gamma, cos, sin = _tables(rng, 7, device)
+    scales = {}
+    if mode == "int8":
+        a, sa = quantize(a, "int8")
+        b, sb = quantize(b, "int8")
+        scales = dict(a_scales=sa, b_scales=sb)
+    inputs = [a, b, gamma, cos, sin, *scales.values()]
+    saved = [t.clone() for t in inputs]
+    y = projection_qk_rope(a, b, gamma, cos, sin, mode, (32, 64, 4, 8), **scales)
+    projected = _projection(a, b, mode, scales.get("a_scales"), scales.get("b_scales"))
+    expected = ref.qk_rope_reference(projected.reshape(7, 3, 128), _f32(gamma), _f32(cos), _f32(sin))["output"]
+    _check(y, expected)
+    if kind == "zeros":
+        assert torch.all(y == 0)
+    for t, s in zip(inputs, saved):
+        assert torch.equal(t, s)
+
+
+@pytest.mark.parametrize("rope_half", [1, 48, 64])
+def test_standalone_norm_rope_reference(rope_half, device):
+    rng = np.random.default_rng(713)
+    p_np = rng.standard_normal((5, 3, 128), dtype=np.float32)
+    p_np[0] = 0
+    p_np[1, :, ::31] *= 100
+    p = torch.from_numpy(p_np.reshape(5, 384)).to(device).to(torch.bfloat16)
+    gamma, cos, sin = _tables(rng, 5, device, rope_half)
+    for threads in (128, 256):
+        y = qk_norm_rope(p, gamma, cos, sin, threads=threads)
+        expected = ref.qk_rope_reference(_f32(p).reshape(5, 3, 128), _f32(gamma), _f32(cos), _f32(sin))["output"]
+        _check(y, expected)
+        assert torch.all(y[:, 0] == 0)
+
+
+def test_split_half_pairs_unrotated_tail_and_head_major_layout(device):
+    p_np = np.ones((3, 2, 128), dtype=np.float32)
+    p_np[:, :, 48:96] = -1
+    p_np[:, 1] *= -1
+    p = torch.from_numpy(p_np.reshape(3, 256)).to(device).to(torch.bfloat16)
+    gamma = torch.ones(128, dtype=torch.bfloat16, device=device)
+    cos = torch.zeros((3, 48), dtype=torch.bfloat16, device=device)
+    sin = torch.ones((3, 48), dtype=torch.bfloat16, device=device)
+    y = qk_norm_rope(p, gamma, cos, sin)
+    expected = p_np.copy()
+    expected[:, :, :48] = -p_np[:, :, 48:96]
+    expected[:, :, 48:96] = p_np[:, :, :48]
+    np.testing.assert_array_equal(_f32(y), expected.transpose(1, 0, 2))
+
+
+def test_no_bf16_norm_intermediate(device):
+    values = np.ones((3, 2, 128), dtype=np.float32)
+    values[:, :, 127] = 2
+    gamma_np = np.ones(128, dtype=np.float32)
+    gamma_np[0] = 1 + 1 / 128
+    p = torch.from_numpy(values.reshape(3, 256)).to(device).to(torch.bfloat16)
+    gamma = torch.from_numpy(gamma_np).to(device).to(torch.bfloat16)
+    cos = torch.full((3, 48), 181 / 256, dtype=torch.bfloat16, device=device)
+    sin = torch.full((3, 48), 181 / 256, dtype=torch.bfloat16, device=device)
+    native = ref.qk_rope_reference(values, _f32(gamma), _f32(cos), _f32(sin))
+    rounded = ref.qk_rope_reference(values, _f32(gamma), _f32(cos), _f32(sin), norm_bf16=True)
+    actual = _f32(qk_norm_rope(p, gamma, cos, sin))
+    np.testing.assert_array_equal(actual[:, :, 0], native["output"][:, :, 0])
+    assert not np.array_equal(actual[:, :, 0], rounded["output"][:, :, 0])
+
+
+@pytest.mark.parametrize("tile", [(16, 64, 4, 3), (32, 128, 4, 1)])
+def test_tiny_projection_preserves_dequant_scales(tile, device):
+    rng = np.random.default_rng(137)
+    m, n, k = 3, 256, 257
+    a_np = rng.integers(-7, 8, size=(m, k), dtype=np.int8)
+    b_np = rng.integers(-7, 8, size=(n, k), dtype=np.int8)
+    sa_np = np.array([1e-4, 1e-5, 5e-5], dtype=np.float32)
+    sb_np = np.full(n, 1e-3, dtype=np.float32)
+    gamma, cos, sin = _tables(rng, m, device)
+    dot = a_np.astype(np.int64) @ b_np.astype(np.int64).T
+    projected = ((dot.astype(np.float32) * sa_np[:, None]) * sb_np[None, :]).reshape(m, n // 128, 128)
+    expected = ref.qk_rope_reference(projected, _f32(gamma), _f32(cos), _f32(sin))["output"]
+    wrong = ref.qk_rope_reference(projected * 2, _f32(gamma), _f32(cos), _f32(sin))["output"]
+    assert ref.metrics(wrong, expected)["relative_l2"] > 0.5
+    y = projection_qk_rope(torch.from_numpy(a_np).to(device), torch.from_numpy(b_np).to(device), gamma, cos, sin,
+                           "int8", tile, a_scales=torch.from_numpy(sa_np).to(device),
+                           b_scales=torch.from_numpy(sb_np).to(device))
+    _check(y, expected, tol=8e-3)
+    assert ref.metrics(_f32(y), wrong)["relative_l2"] > 0.4
+
+
+def test_qk_configuration_shape(device):
+    """x bf16 [9914, 4096], Wq [4096, 4096] ~N(0, 0.02), 32 heads x 128, eps 1e-6, gamma ~1+N(0,.02),
+    RoPE base 10000 over positions 0..9913 (R = 64); online INT8 and BF16 projections."""
+    m, k, n = 9914, 4096, 4096
+    g = torch.Generator(device=device).manual_seed(43)
+    x = torch.randn((m, k), generator=g, device=device).to(torch.bfloat16)
+    w = (0.02 * torch.randn((n, k), generator=g, device=device)).to(torch.bfloat16)
+    gamma = (1 + 0.02 * torch.randn(128, generator=g, device=device)).to(torch.bfloat16)
+    inv_freq = 10000.0 ** (-torch.arange(0, 64, dtype=torch.float64) * 2 / 128)
+    angles = torch.arange(m, dtype=torch.float64)[:, None] * inv_freq[None, :]
+    cos = torch.cos(angles).float().to(device).to(torch.bfloat16)
+    sin = torch.sin(angles).float().to(device).to(torch.bfloat16)
+    rows = ref.sample_indices(m)
+    for mode in ("int8", "bf16"):
+        if mode == "int8":
+            aq, sa = quantize(x, "int8")
+            wq, sw = quantize(w, "int8")
+            y = projection_qk_rope(aq, wq, gamma, cos, sin, "int8", a_scales=sa, b_scales=sw, epsilon=1e-6)
+            staged = qk_norm_rope(gemm(aq, wq, "int8", a_scales=sa, b_scales=sw, output_dtype=torch.bfloat16),
+                                  gamma, cos, sin, epsilon=1e-6)
+            dot = np_of(aq)[rows].astype(np.int64) @ np_of(wq).astype(np.int64).T
+            proj = (dot.astype(np.float32) * np_of(sa)[rows][:, None]) * np_of(sw)[None, :]
+        else:
+            y = projection_qk_rope(x, w, gamma, cos, sin, "bf16", epsilon=1e-6)
+            staged = qk_norm_rope(gemm(x, w, "bf16", output_dtype=torch.bfloat16), gamma, cos, sin, epsilon=1e-6)
+            proj = _f32(x[rows]).astype(np.float64) @ _f32(w).astype(np.float64).T
+        assert y.shape == (32, m, 128)
+        assert torch.equal(y, staged)
+        expected = ref.qk_rope_reference(proj.reshape(len(rows), 32, 128), _f32(gamma), _f32(cos)[rows],
+                                         _f32(sin)[rows], epsilon=1e-6)["output"]
+        _check(y[:, rows], expected)
+        assert math.isfinite(float(y.float().abs().max()))
