@@ -30,7 +30,7 @@ M, K, N = 4096, 16384, 4096
 SEED = 29
 PEAK_INT8_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
-TRAFFIC_FILE = REPO / "profiles" / "gemm_i8_ffn_down_traffic.json"
+TRAFFIC_FILE = REPO / "profiles" / "traffic.json"
 
 
 def log(*a):
@@ -87,6 +87,8 @@ def main():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample duration")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     p.add_argument("--no-torch", action="store_true", help="skip the BF16 torch baseline (profiling runs)")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="only run a 256 MiB device copy x5 (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = p.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -103,6 +105,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.ones(128 * 1024 * 1024, dtype=torch.bfloat16, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] copied 256 MiB x5")
+        return
     log(f"[bench] inputs: A bf16 [{M},{K}], W bf16 [{N},{K}], seed {SEED}")
     a, w = make_inputs(torch, dev)
     wq, ws = quantize(w, "int8")  # offline weight preparation, untimed
@@ -148,8 +158,11 @@ def main():
         f"quant {quant_avg:.4f} ms ({quant_gbs:.0f} GB/s)")
 
     traffic = None
-    if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    quant_traffic = None
+    if TRAFFIC_FILE.exists():  # scaled FETCH_SIZE + WRITE_SIZE per launch from the rocprofv3 --pmc runs
+        measured = json.loads(TRAFFIC_FILE.read_text())
+        traffic = measured.get("gemm_i8_ffn_down", {}).get("hbm_bytes_per_launch")
+        quant_traffic = measured.get("quantize_rows_int8_ffn_down", {}).get("hbm_bytes_per_launch")
 
     result = {
         "metric": "W8A8 TOPS and ms at M=4096 FFN-down incl. online quant; % INT8 MFMA peak",
@@ -194,6 +207,7 @@ def main():
                 "bytes_per_launch": quant_bytes,
                 "achieved_GBps": quant_gbs,
                 "frac_of_hbm_peak": quant_gbs / PEAK_HBM_GBS,
+                "traffic": quant_traffic,
             },
             "gemm_i8": {"avg_ms": gemm_avg, "achieved_TOPS": gemm_tops, "frac_of_int8_peak": gemm_tops / PEAK_INT8_TOPS},
         },
@@ -215,6 +229,19 @@ def main():
         bf16_ms = s0.elapsed_time(s1) / 10
         result["bf16_torch_linear"] = {"ms": bf16_ms, "TFLOPs": ops / (bf16_ms * 1e-3) / 1e12,
                                        "speedup_of_w8a8_online": bf16_ms / ms_per_step}
+        # hipBLASLt INT8 GEMM on the same quantized operands (INT32 output, no scale epilogue).
+        wq_t = wq.t()
+        for _ in range(3):
+            torch._int_mm(aq, wq_t)
+        torch.cuda.synchronize()
+        s0.record()
+        for _ in range(10):
+            torch._int_mm(aq, wq_t)
+        s1.record()
+        torch.cuda.synchronize()
+        i8_ms = s0.elapsed_time(s1) / 10
+        result["hipblaslt_int8_int_mm"] = {"ms": i8_ms, "TOPS": ops / (i8_ms * 1e-3) / 1e12,
+                                           "m5k_gemm_speedup": i8_ms / gemm_avg}
 
     if not args.no_cpu:
         log("[bench] cpu baseline")

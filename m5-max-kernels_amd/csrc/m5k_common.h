@@ -112,6 +112,60 @@ __device__ __forceinline__ uint32_t quant_encode(float x, float scale) {
   }
 }
 
+// Row-constant INT8 encoder state: the scale, its correctly rounded reciprocal, and `exact`
+// when the reciprocal is unsafe (scale below 2^-100, where 1/scale may overflow): then every
+// element takes the IEEE division.
+struct I8Scale {
+  float scale;
+  float inv;
+  bool exact;
+};
+
+__device__ __forceinline__ I8Scale i8_scale(float scale) {
+  return I8Scale{scale, 1.0f / scale, scale < 0x1p-100f};
+}
+
+__device__ __forceinline__ uint32_t i8_clamp_code(float r) {
+  const float c = fminf(fmaxf(r, -127.0f), 127.0f);
+  return static_cast<uint32_t>(static_cast<int>(c)) & 0xFFu;
+}
+
+// INT8 codes of N values (N % 4 == 0) packed 4 per word, bit-identical to
+// clamp(rint_even(fl(x / scale)), -127, 127) for every x of a row whose |x| <= peak.
+// Fast path: q0 = fl(x * inv).  With scale = fl(peak / 127), |x / scale| <= 127.01, and
+// |q0 - x/scale| <= 127.01 * (2^-23 + 2^-48) < 2^-16, so rint(q0) == rint(x/scale) unless a
+// rounding boundary n + 1/2 lies within 2^-16 of q0.  Clamping to [-127, 127] before the
+// rounding gives the same code.  Adding 1.5 * 2^23 rounds the clamped value to an integer
+// (round-half-even) and leaves its two's-complement low byte in the low byte of the sum's
+// bits.  If any element of the group lies within 2^-15 of a rounding boundary
+// (|qc - rint(qc)| >= 1/2 - 2^-15, exact ties included) the whole group takes the IEEE
+// division instead; one branch per group keeps the common path at about six VALU ops.
+template <int N>
+__device__ __forceinline__ void encode_i8(const float (&x)[N], const I8Scale& s, uint32_t (&out)[N / 4]) {
+  constexpr float kRound = 0x1.8p23f;
+  uint32_t t[N];
+  float dev = s.exact ? 1.0f : 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float qc = fminf(fmaxf(x[i] * s.inv, -127.0f), 127.0f);
+    const float biased = qc + kRound;
+    dev = fmaxf(dev, fabsf(qc - (biased - kRound)));
+    t[i] = __float_as_uint(biased);
+  }
+  if (dev >= 0.5f - 0x1p-15f) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = __float_as_uint(fminf(fmaxf(rintf(x[i] / s.scale), -127.0f), 127.0f) + kRound);
+  }
+#pragma unroll
+  for (int w = 0; w < N / 4; ++w) {
+    // v_perm_b32 picks byte 0 of each operand: selector bytes 0 and 4 address src1.b0 and src0.b0,
+    // 0x0C yields zero.
+    const uint32_t lo = __builtin_amdgcn_perm(t[4 * w + 1], t[4 * w], 0x0C0C0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(t[4 * w + 3], t[4 * w + 2], 0x04000C0Cu);
+    out[w] = lo | hi;
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ float quant_scale(float peak) {
   return peak == 0.0f ? 1.0f : peak / (MODE == M5K_QUANT_FP8 ? 448.0f : 127.0f);

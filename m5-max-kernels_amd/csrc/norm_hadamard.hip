@@ -211,8 +211,8 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p) {
     }
   }
   peak = block_max<kWaves>(peak, red);
-  const float scale = quant_scale<M5K_QUANT_INT8>(peak);
-  if (threadIdx.x == 0) p.scales[row] = scale;
+  const I8Scale enc = i8_scale(quant_scale<M5K_QUANT_INT8>(peak));
+  if (threadIdx.x == 0) p.scales[row] = enc.scale;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
@@ -220,13 +220,12 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p) {
       uint2* out = reinterpret_cast<uint2*>(p.q + row * p.k + c * EPC);
 #pragma unroll
       for (int t = 0; t < EPC / 8; ++t) {
-        uint32_t lo = 0, hi = 0;
+        float g[8];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          lo |= quant_encode<M5K_QUANT_INT8>(v[i * EPC + 8 * t + b], scale) << (8 * b);
-          hi |= quant_encode<M5K_QUANT_INT8>(v[i * EPC + 8 * t + 4 + b], scale) << (8 * b);
-        }
-        out[t] = make_uint2(lo, hi);
+        for (int b = 0; b < 8; ++b) g[b] = v[i * EPC + 8 * t + b];
+        uint32_t w[2];
+        encode_i8<8>(g, enc, w);
+        out[t] = make_uint2(w[0], w[1]);
       }
     }
   }

@@ -71,6 +71,64 @@ def test_ffn_down_activation_full_size_bit_exact(mode, device):
     np.testing.assert_array_equal(np_of(q), rq)
 
 
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("rows,k", [(2048, 2048), (2051, 4096), (3001, 8192), (2049, 16384), (2500, 1000)])
+def test_many_rows_bit_exact(mode, dtype, rows, k, device):
+    """Long batches at each register-chunk width (K 1000..16384), odd row counts, outlier
+    columns and one all-zero row."""
+    g = torch.Generator(device="cpu").manual_seed(rows + k)
+    x = torch.randn((rows, k), generator=g, dtype=torch.float32)
+    x[:, ::97] *= 40
+    x[rows // 3] = 0  # one all-zero row mid-stream
+    xt = x.to(device).to(DTYPES[dtype])
+    q, s = quantize(xt, mode)
+    src = bits_of(xt) if dtype == "bf16" else xt.float().cpu().numpy()
+    rq, rs = ref.c_quantize_rows(src, mode)
+    np.testing.assert_array_equal(np_of(s), rs)
+    np.testing.assert_array_equal(np_of(q), rq)
+
+
+@pytest.mark.parametrize("dtype,m", [("fp16", 7), ("fp32", 7), ("fp32", 4095)])
+def test_int8_dense_ties_bit_exact(dtype, m, device):
+    """Rows with peak 127 m make the scale exactly m, so x = m (n + 1/2) is an exact tie of
+    x / scale; x * fl(1/m) misses the tie for 78 (m = 7) or 126 (m = 4095) of the 254 values,
+    so those elements must take the division path.  Neighbours one ulp either side of each tie
+    check the rounding just off the boundary."""
+    n = np.arange(-127, 127, dtype=np.float32)
+    ties = np.float32(m) * (n + np.float32(0.5))
+    row = np.concatenate([[127.0 * m], ties, np.nextafter(ties, np.float32(np.inf)), np.nextafter(ties, -np.float32(np.inf))])
+    row = np.resize(row.astype(np.float32), 2048)
+    x = np.stack([row, -row, np.roll(row, 5)])
+    xt = torch.from_numpy(x).to(device).to(DTYPES[dtype])
+    q, s = quantize(xt, "int8")
+    x32 = xt.float().cpu().numpy()
+    rq, rs = ref.c_quantize_rows(x32, "int8")
+    assert np.all(rs == np.float32(m))
+    fast = np.clip(np.rint(x32 * (np.float32(1) / np.float32(m))), -127, 127).astype(np.int8)
+    assert np.count_nonzero(fast != rq) > 0  # the reciprocal alone would fail this row
+    np.testing.assert_array_equal(np_of(s), rs)
+    np.testing.assert_array_equal(np_of(q), rq)
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_nan_ignored_by_row_peak(dtype, device):
+    """The row peak ignores NaN like the reference's max (quantize.metal:7); the codes of the
+    finite elements are unaffected.  (A NaN's own code has no defined value in the reference.)"""
+    x = _input("outliers", (6, 4096), seed=5)
+    x[0, 17] = np.nan
+    x[1, :8] = np.nan
+    x[2, 4095] = np.nan
+    x[3, ::2] = np.nan
+    xt = torch.from_numpy(x).to(device).to(DTYPES[dtype])
+    q, s = quantize(xt, "int8")
+    x32 = xt.float().cpu().numpy()
+    rq, rs = ref.c_quantize_rows(x32, "int8")
+    np.testing.assert_array_equal(np_of(s), rs)
+    finite = np.isfinite(x32)
+    np.testing.assert_array_equal(np_of(q)[finite], rq[finite])
+
+
 def test_round_half_even_kat(kats, device):
     kat = kats["int8_round_half_even"]
     x = torch.tensor([kat["row"]] * 3, dtype=torch.float32, device=device)
