@@ -79,6 +79,194 @@ def cpu_baseline(torch, a, wq, ws, y, target_s):
     }
 
 
+def time_op(torch, fn, reps=20, warm=3):
+    """Device time of fn: HIP events on the current stream around each of `reps` launches."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    ts = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+    return {"avg_ms": statistics.fmean(ts), "p10_ms": ts[len(ts) // 10], "p90_ms": ts[(9 * len(ts)) // 10]}
+
+
+def _gemm_case(torch, dev, m, k, n, seed, mode="int8", outlier_every=None):
+    """Online W quantized offline; step = quantize(A) + GEMM -> BF16."""
+    from m5kernels_amd import gemm, quantize
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a = torch.randn((m, k), generator=g, device=dev)
+    if outlier_every:
+        a[:, ::outlier_every] *= 50.0
+    a = a.to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wq, ws = quantize(w, mode)
+    aq, sa = quantize(a, mode)
+    ops = 2.0 * m * n * k
+
+    def online():
+        q, s = quantize(a, mode)
+        return gemm(q, wq, mode, a_scales=s, b_scales=ws, output_dtype=torch.bfloat16)
+
+    step = time_op(torch, online)
+    only = time_op(torch, lambda: gemm(aq, wq, mode, a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16))
+    return {
+        "shape": {"m": m, "k": k, "n": n},
+        "mode": mode,
+        "online_ms": step["avg_ms"],
+        "online_TOPS": ops / (step["avg_ms"] * 1e-3) / 1e12,
+        "gemm_ms": only["avg_ms"],
+        "gemm_TOPS": ops / (only["avg_ms"] * 1e-3) / 1e12,
+        "gemm_frac_of_peak": ops / (only["avg_ms"] * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+        "online_p10_p90_ms": [step["p10_ms"], step["p90_ms"]],
+    }
+
+
+def _hadamard_case(torch, dev):
+    """FFN-down with a normalized block-128 Hadamard (signs +1): W rotated + quantized offline,
+    A rotated in FP32 and quantized online in one kernel, then the W8A8 GEMM."""
+    from m5kernels_amd import gemm, quantize, rotate, rotate_quantize
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    a = torch.randn((M, K), generator=g, device=dev)
+    a[:, ::1024] *= 50.0
+    a = a.to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    signs = torch.ones(K, dtype=torch.int8, device=dev)
+    wq, ws = quantize(rotate(w, 128, signs), "int8")
+    ops = 2.0 * M * N * K
+
+    def online():
+        q, s = rotate_quantize(a, 128, signs)
+        return gemm(q, wq, "int8", a_scales=s, b_scales=ws, output_dtype=torch.bfloat16)
+
+    step = time_op(torch, online)
+    rq = time_op(torch, lambda: rotate_quantize(a, 128, signs))
+    nbytes = 3 * M * K + 4 * M
+    return {
+        "online_ms": step["avg_ms"],
+        "online_TOPS": ops / (step["avg_ms"] * 1e-3) / 1e12,
+        "rotate_quantize_ms": rq["avg_ms"],
+        "rotate_quantize_GBps": nbytes / (rq["avg_ms"] * 1e-3) / 1e9,
+        "rotate_quantize_frac_of_hbm_peak": nbytes / (rq["avg_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS,
+    }
+
+
+def _prep_case(torch, dev, m, k=4096, tables=2):
+    """Fused AdaLN prep (LayerNorm, H128, P per-batch tables, BF16 boundary) with and without
+    the gated residual update, the staged comparators, and the W8A8 GEMM it feeds."""
+    from m5kernels_amd import (fused_gated_residual_norm_hadamard_quantize, fused_norm_hadamard_quantize, gated_residual_add,
+                               gemm, quantize, rotate_quantize, unfused_norm)
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    bf = torch.bfloat16
+    res = torch.randn((m, k), generator=g, device=dev).to(bf)
+    branch = torch.randn((m, k), generator=g, device=dev).to(bf)
+    gate = (torch.randn((tables, k), generator=g, device=dev) * 0.1).to(bf)
+    scale = (torch.randn((tables, k), generator=g, device=dev) * 0.1).to(bf)
+    shift = (torch.randn((tables, k), generator=g, device=dev) * 0.1).to(bf)
+    gamma = (1 + 0.1 * torch.randn((k,), generator=g, device=dev)).to(bf)
+    row_map = (torch.arange(m, device=dev, dtype=torch.int32) * tables // m).to(torch.int32)
+    signs = torch.ones(k, dtype=torch.int8, device=dev)
+    kw = dict(norm="layer", epsilon=1e-5, round_output="input", row_map=row_map)
+    gated = time_op(torch, lambda: fused_gated_residual_norm_hadamard_quantize(
+        res, branch, gate, gamma, scale, shift, signs, 128, gate_row_map=row_map, **kw))
+    plain = time_op(torch, lambda: fused_norm_hadamard_quantize(res, gamma, scale, shift, signs, 128, **kw))
+
+    def staged():
+        r = gated_residual_add(res, branch, gate, gate_row_map=row_map)
+        y = unfused_norm(r, gamma, scale, shift, **kw)
+        return rotate_quantize(y, 128, signs)
+
+    staged_t = time_op(torch, staged)
+    w = (torch.randn((k, k), generator=g, device=dev) * 0.02).to(bf)
+    wq, ws = quantize(w, "int8")
+    q, s = fused_norm_hadamard_quantize(res, gamma, scale, shift, signs, 128, **kw)
+    gemm_t = time_op(torch, lambda: gemm(q, wq, "int8", a_scales=s, b_scales=ws, output_dtype=bf))
+    table_bytes = 2 * k + 3 * 2 * tables * k + 4 * m + k  # gamma, gate/scale/shift tables, row map, signs
+    gated_bytes = 7 * m * k + 4 * m + table_bytes
+    plain_bytes = 3 * m * k + 4 * m + table_bytes
+    gbs = lambda b, t: b / (t * 1e-3) / 1e9  # noqa: E731
+    return {
+        "m": m,
+        "k": k,
+        "tables": tables,
+        "gated_fused_ms": gated["avg_ms"],
+        "gated_fused_GBps": gbs(gated_bytes, gated["avg_ms"]),
+        "gated_fused_frac_of_hbm_peak": gbs(gated_bytes, gated["avg_ms"]) / PEAK_HBM_GBS,
+        "gated_bytes_per_launch": gated_bytes,
+        "fused_ms": plain["avg_ms"],
+        "fused_GBps": gbs(plain_bytes, plain["avg_ms"]),
+        "fused_frac_of_hbm_peak": gbs(plain_bytes, plain["avg_ms"]) / PEAK_HBM_GBS,
+        "fused_bytes_per_launch": plain_bytes,
+        "staged_gated_ms": staged_t["avg_ms"],
+        "staged_over_fused": staged_t["avg_ms"] / gated["avg_ms"],
+        "w8a8_gemm_4096_ms": gemm_t["avg_ms"],
+        "w8a8_gemm_4096_TOPS": 2.0 * m * k * k / (gemm_t["avg_ms"] * 1e-3) / 1e12,
+    }
+
+
+def _qk_case(torch, dev, m=9914, k=4096, n=4096):
+    """Q projection + per-head RMSNorm + split-half RoPE (R = 64, base 10000, positions 0..m-1),
+    head-major BF16 [32, m, 128]: INT8 online (quantize + fused projection) and BF16 modes, and
+    the staged postprocess on a BF16 projection."""
+    from m5kernels_amd import gemm, projection_qk_rope, qk_norm_rope, quantize
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    bf = torch.bfloat16
+    x = torch.randn((m, k), generator=g, device=dev).to(bf)
+    w = (torch.randn((n, k), generator=g, device=dev) * 0.02).to(bf)
+    gamma = (1 + 0.02 * torch.randn((128,), generator=g, device=dev)).to(bf)
+    theta = 10000.0 ** (-torch.arange(64, device=dev, dtype=torch.float64) * 2 / 128)
+    ang = torch.arange(m, device=dev, dtype=torch.float64)[:, None] * theta[None, :]
+    cos, sin = ang.cos().float().to(bf), ang.sin().float().to(bf)
+    wq, ws = quantize(w, "int8")
+    ops = 2.0 * m * n * k
+
+    def int8_online():
+        q, s = quantize(x, "int8")
+        return projection_qk_rope(q, wq, gamma, cos, sin, "int8", a_scales=s, b_scales=ws, epsilon=1e-6)
+
+    t8 = time_op(torch, int8_online)
+    tb = time_op(torch, lambda: projection_qk_rope(x, w, gamma, cos, sin, "bf16", epsilon=1e-6))
+    proj = gemm(x, w, "bf16", output_dtype=bf)
+    tpost = time_op(torch, lambda: qk_norm_rope(proj, gamma, cos, sin, epsilon=1e-6))
+    post_bytes = 2 * m * n * 2 + 2 * 2 * m * 64 + 2 * 128
+    return {
+        "m": m,
+        "int8_online_ms": t8["avg_ms"],
+        "int8_online_TOPS": ops / (t8["avg_ms"] * 1e-3) / 1e12,
+        "bf16_fused_ms": tb["avg_ms"],
+        "bf16_fused_TFLOPs": ops / (tb["avg_ms"] * 1e-3) / 1e12,
+        "staged_postprocess_ms": tpost["avg_ms"],
+        "staged_postprocess_GBps": post_bytes / (tpost["avg_ms"] * 1e-3) / 1e9,
+    }
+
+
+def extras(torch, dev):
+    """Every other configuration: parity-test shapes timed on the same GPU (not the headline)."""
+    out = {}
+    cases = [
+        ("ffn_down_fp8_online", lambda: _gemm_case(torch, dev, M, K, N, SEED, "fp8", 1024)),
+        ("ffn_down_h128_int8_online", lambda: _hadamard_case(torch, dev)),
+        ("q_proj_4096_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 4096, SEED)),
+        ("ffn_up_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 16384, SEED)),
+        ("fused_prep_m4096", lambda: _prep_case(torch, dev, 4096)),
+        ("fused_prep_m9914", lambda: _prep_case(torch, dev, 9914)),
+        ("qk_rope_m9914", lambda: _qk_case(torch, dev)),
+    ]
+    for name, fn in cases:
+        log(f"[bench] extra {name}")
+        out[name] = fn()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
@@ -87,6 +275,7 @@ def main():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample duration")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     p.add_argument("--no-torch", action="store_true", help="skip the BF16 torch baseline (profiling runs)")
+    p.add_argument("--no-extras", action="store_true", help="skip the other configurations (profiling runs)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a 256 MiB device copy x5 (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = p.parse_args()
@@ -145,6 +334,13 @@ def main():
     wall_ms = (time.perf_counter() - t0) * 1e3
     total_ms = start.elapsed_time(end)
     quant_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    host = []
+    for _ in range(min(steps, 20)):  # synchronized host wall per step (the reference's measure)
+        h0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        host.append((time.perf_counter() - h0) * 1e3)
+    host.sort()
     gemm_ms = [e[1].elapsed_time(e[2]) for e in ev]
     ms_per_step = max(total_ms, wall_ms) / steps
     ops = 2.0 * M * N * K
@@ -211,7 +407,14 @@ def main():
             },
             "gemm_i8": {"avg_ms": gemm_avg, "achieved_TOPS": gemm_tops, "frac_of_int8_peak": gemm_tops / PEAK_INT8_TOPS},
         },
-        "timing": {"event_total_ms": total_ms, "wall_ms": wall_ms, "method": "HIP events on the launch stream"},
+        "timing": {
+            "event_total_ms": total_ms,
+            "wall_ms": wall_ms,
+            "method": "HIP events on the launch stream; value uses max(event, host wall) over the timed steps",
+            "host_sync_ms_per_step": {"median": host[len(host) // 2], "p10": host[len(host) // 10],
+                                      "p90": host[(9 * len(host)) // 10]},
+            "gemm_p10_p90_ms": [sorted(gemm_ms)[steps // 10], sorted(gemm_ms)[(9 * steps) // 10]],
+        },
     }
 
     if not args.no_torch:
@@ -242,6 +445,9 @@ def main():
         i8_ms = s0.elapsed_time(s1) / 10
         result["hipblaslt_int8_int_mm"] = {"ms": i8_ms, "TOPS": ops / (i8_ms * 1e-3) / 1e12,
                                            "m5k_gemm_speedup": i8_ms / gemm_avg}
+
+    if not args.no_extras:
+        result["extras"] = extras(torch, dev)
 
     if not args.no_cpu:
         log("[bench] cpu baseline")
