@@ -8,9 +8,10 @@
 // Register layout: a lane holds EPC = max(8, B/64) consecutive elements of a block, so
 // one block spans LPB = B/EPC <= 64 consecutive lanes.  Strides below EPC stay inside
 // a lane's registers; strides EPC..B/2 are lane-xor exchanges within the LPB-lane group
-// (the upper lane of a pair computes lower - upper).  Each stage output is one FP32
-// add or subtract of its two inputs, so the result is independent of which lane does
-// the work and bit-identical to a sequential FP32 evaluation of the same stages.
+// (the upper lane of a pair computes lower - upper, as an FMA with -1).  Each stage output
+// is one correctly rounded FP32 sum or difference of its two inputs, so the result is
+// independent of which lane does the work and bit-identical to a sequential FP32
+// evaluation of the same stages.
 #pragma once
 
 #include "m5k_common.h"
@@ -55,12 +56,11 @@ __device__ __forceinline__ void butterflies(float (&v)[Shape<B>::EPC]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 1; m < LPB; m <<= 1) {
-    const bool upper = (lane & m) != 0;
+    // fma(+-1, v, peer) is the single rounding of v + peer (lower lane) or peer - v (upper
+    // lane): the same bits as the add or subtract, in one VALU op instead of add, sub, select.
+    const float sgn = (lane & m) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int r = 0; r < EPC; ++r) {
-      const float peer = __shfl_xor(v[r], m, 64);
-      v[r] = upper ? peer - v[r] : v[r] + peer;
-    }
+    for (int r = 0; r < EPC; ++r) v[r] = __builtin_fmaf(sgn, v[r], __shfl_xor(v[r], m, 64));
   }
   constexpr float inv = inv_sqrt_block<B>();
 #pragma unroll

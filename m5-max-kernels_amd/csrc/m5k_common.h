@@ -33,11 +33,20 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
 }
 
 // FP32 -> BF16 round to nearest even, the producer-side cast of the reference
-// (qk_rope_reference.py:37-42 bit formula; finite inputs).
+// (qk_rope_reference.py:37-42: (u + 0x7FFF + ((u >> 16) & 1)) >> 16 on finite inputs).
+// gfx950's v_cvt_pk_bf16_f32 computes exactly that for every finite FP32 bit pattern,
+// denormals included (checked exhaustively on MI355X), one instruction per pair.
+typedef __bf16 m5k_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float m5k_f32x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two values to packed BF16 (lo in bits 0-15).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  const m5k_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, m5k_bf16x2));
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
@@ -172,19 +181,40 @@ __device__ __forceinline__ float quant_scale(float peak) {
 }
 
 // ---- wave64 reductions -------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+// DPP lane movement of v (0 where the row mask leaves a lane unwritten).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
 }
 
+// Sum over the 64 lanes, the result in every lane.  Fixed tree: lane pairs (xor 1), pairs
+// of pairs (xor 2), quads across each half-row (row_half_mirror), halves across each row
+// (row_mirror); then row 1 += row 0 and row 3 += row 2 (row_bcast15), row 3 += rows 0-1
+// (row_bcast31); lane 63 holds (r2 + r3) + (r0 + r1).  One DPP add per step.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m <= 32; m <<= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  v += dpp_move<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
+  v += dpp_move<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Block-wide reductions over NWAVES waves via LDS; every thread gets the result.
+// Maximum over the 64 lanes of non-negative values (absolute peaks), same movement pattern;
+// lanes a row mask leaves unwritten contribute 0.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  v = fmaxf(v, dpp_move<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_move<0x143, 0xC>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Block-wide reductions over NWAVES waves through the NWAVES-float LDS slot `lds`; every
+// thread gets the result.  One barrier: each reduction in a workgroup needs its own slot.
 template <int NWAVES>
 __device__ __forceinline__ float block_max(float v, float* lds) {
   v = wave_max(v);
@@ -194,7 +224,6 @@ __device__ __forceinline__ float block_max(float v, float* lds) {
   float r = lds[0];
 #pragma unroll
   for (int w = 1; w < NWAVES; ++w) r = fmaxf(r, lds[w]);
-  __syncthreads();
   return r;
 }
 
@@ -207,7 +236,6 @@ __device__ __forceinline__ float block_sum(float v, float* lds) {
   float r = lds[0];
 #pragma unroll
   for (int w = 1; w < NWAVES; ++w) r += lds[w];
-  __syncthreads();
   return r;
 }
 

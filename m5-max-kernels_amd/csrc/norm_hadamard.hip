@@ -4,6 +4,9 @@
 //   stats    RMS: var = sum(r^2)/K            LayerNorm: mean = sum(r)/K, var = sum((r-mean)^2)/K
 //            inv = 1 / sqrt(var + eps)         (IEEE division and square root)
 //   modulate y = O(((r - mean) * inv * gamma[j]) * (1 + scale[t + j]) + shift[t + j])
+// The squares are accumulated and the last multiply-add of the modulation is evaluated as
+// fused multiply-adds (one rounding each), the contraction the reference's Metal build
+// applies by default; the reference pins these stages only to +-1 code.
 //   rotate   z = blockdiag(H_B) (y * signs)   (natural-order Sylvester, FP32, * 1/sqrt(B))
 //   quantize s = max|z| / 127 (1 if 0); q = clamp(rint_even(z / s), -127, 127)
 //
@@ -13,9 +16,12 @@
 // (norm_modulate.metal) run the same per-element arithmetic and the same reduction tree, so
 // staged rotate(quantize(...)) reproduces the fused codes bit for bit (blocks <= 512).
 //
-// Layout: one workgroup (4 wave64) per row; a lane owns CPT chunks of EPC consecutive
-// elements (chunk c = tid + 256*i), the whole row stays in VGPRs: HBM traffic is the
-// minimum 2K (+2K branch, +2K R_next) + K + 4 bytes per row plus the parameter tables.
+// Layout: one workgroup of 4 wave64 per row.  A lane owns NCH chunks of EPC consecutive
+// elements (chunk c = tid + 256*i) and the whole row stays in VGPRs: HBM traffic is the
+// minimum 2K (+2K branch, +2K R_next) + K + 4 bytes per row plus the parameter tables.  At
+// K = 4096 a lane holds 16 values, which keeps register use low enough for 8 resident
+// workgroups per CU; a one-wave-per-row layout (64 values per lane) measured slower for lack
+// of resident waves.
 #include "hadamard_core.h"
 
 namespace m5k {
@@ -62,188 +68,295 @@ __device__ __forceinline__ void load8(const void* base, int64_t e, float (&v)[8]
     const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v[2 * i] = DT == M5K_BF16 ? bf16_bits_to_f32(w[i] & 0xFFFFu) : f16_bits_to_f32(w[i] & 0xFFFFu);
-      v[2 * i + 1] = DT == M5K_BF16 ? bf16_bits_to_f32(w[i] >> 16) : f16_bits_to_f32(w[i] >> 16);
+      if constexpr (DT == M5K_BF16) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      } else {
+        v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
+// Round 8 values through dtype DT in place (the O(...) / R(...) cast) and return their
+// storage words; BF16 pairs take one v_cvt_pk_bf16_f32 each.
+template <int DT>
+__device__ __forceinline__ void round8(float (&v)[8], uint32_t (&w)[8 * dtype_bytes<DT>() / 4]) {
+  if constexpr (DT == M5K_F32) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __float_as_uint(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == M5K_BF16) {
+        w[i] = f32x2_to_bf16x2(v[2 * i], v[2 * i + 1]);
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      } else {
+        const uint32_t lo = f32_to_f16_bits(v[2 * i]), hi = f32_to_f16_bits(v[2 * i + 1]);
+        w[i] = lo | (hi << 16);
+        v[2 * i] = f16_bits_to_f32(lo);
+        v[2 * i + 1] = f16_bits_to_f32(hi);
+      }
     }
   }
 }
 
 template <int DT>
-__device__ __forceinline__ void store8(void* base, int64_t e, const float (&v)[8]) {
+__device__ __forceinline__ void store_words8(void* base, int64_t e, const uint32_t (&w)[8 * dtype_bytes<DT>() / 4]) {
   uint4* p = reinterpret_cast<uint4*>(static_cast<uint8_t*>(base) + e * dtype_bytes<DT>());
-  if constexpr (DT == M5K_F32) {
-    p[0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
-    p[1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7]));
-  } else {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = DT == M5K_BF16 ? f32_to_bf16_bits(v[2 * i]) : f32_to_f16_bits(v[2 * i]);
-      const uint32_t hi = DT == M5K_BF16 ? f32_to_bf16_bits(v[2 * i + 1]) : f32_to_f16_bits(v[2 * i + 1]);
-      w[i] = lo | (hi << 16);
-    }
-    p[0] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
+  p[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  if constexpr (DT == M5K_F32) p[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
-// Row input for chunk c (8 elements at column j = 8c): X, or the gated residual update,
-// rounded to the residual dtype and written to R_next.
+// Which lanes own a row and how they reduce.  Chunk c of a row lives on lane c % kLanes.
+struct GroupRow {  // one workgroup of 4 wave64 per row
+  static constexpr int kLanes = kThreads;
+  static constexpr int kRowsPerGroup = 1;
+  __device__ static int64_t row() { return blockIdx.x; }
+  __device__ static int lane() { return threadIdx.x; }
+  __device__ static float sum(float v, float* red) { return block_sum<kWaves>(v, red); }
+  __device__ static float max(float v, float* red) { return block_max<kWaves>(v, red); }
+};
+
+// Row input for 8 elements at column j: X, or the gated residual update rounded to the
+// residual dtype and written to R_next (FP32 product, then add, then one cast).
 template <int XDT, int PDT, bool GATED>
-__device__ __forceinline__ void load_row_chunk(const PrepParams& p, int64_t row, int64_t j, float (&v)[8]) {
+__device__ __forceinline__ void load_input8(const PrepParams& p, int64_t row, int64_t goff, int64_t j,
+                                            float (&v)[8]) {
   const int64_t e = row * p.k + j;
   load8<XDT>(p.x, e, v);
   if constexpr (GATED) {
     float b[8], g[8];
     load8<XDT>(p.branch, e, b);
-    const int64_t goff = p.gate_map ? static_cast<int64_t>(p.gate_map[row]) * p.k : 0;
     load8<PDT>(p.gate, goff + j, g);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = round_through<XDT>(v[i] + b[i] * g[i]);
-    store8<XDT>(p.r_next, e, v);
+    for (int i = 0; i < 8; ++i) v[i] = v[i] + b[i] * g[i];
+    uint32_t w[8 * dtype_bytes<XDT>() / 4];
+    round8<XDT>(v, w);
+    store_words8<XDT>(p.r_next, e, w);
   }
 }
 
-// Row statistics over the register-resident row: (mean, inv).  The reduction tree (lane
-// partials in chunk order, wave xor-butterfly, waves summed in order) is shared by the fused
-// and staged kernels.
-template <int NV>
-__device__ __forceinline__ void row_stats(const float (&v)[NV], const bool (&live)[NV / 8], int64_t k, int layer,
-                                          float eps, float* red, float& mean, float& inv) {
+// Row statistics over the register-resident row.  LayerNorm centres v in place (v - mean,
+// the reference's first modulation term, computed once); RMS leaves v as is.  Returns
+// inv = 1 / sqrt(var + eps).  Reduction tree: lane partials in chunk order, then the
+// layout's reduction (wave xor-butterfly; for GroupRow the 4 wave sums in order).  Chunks
+// past the row hold zeros and are re-zeroed after centring.
+template <class L, int NV>
+__device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV / 8], int64_t k, int layer,
+                                           float eps, float* red) {
   const float kf = static_cast<float>(k);
   float first = 0.0f;
+  if (layer) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) first += layer ? v[i] : v[i] * v[i];
-  first = block_sum<kWaves>(first, red) / kf;
-  mean = layer ? first : 0.0f;
+    for (int i = 0; i < NV; ++i) first += v[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) first = __builtin_fmaf(v[i], v[i], first);
+  }
+  first = L::sum(first, red) / kf;  // slot 0
   float var = first;
   if (layer) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] -= first;
+#pragma unroll
+    for (int c = 0; c < NV / 8; ++c) {
+      if (!live[c]) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[8 * c + r] = 0.0f;
+      }
+    }
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const float c = live[i / 8] ? v[i] - mean : 0.0f;
-      acc += c * c;
-    }
-    var = block_sum<kWaves>(acc, red) / kf;
+    for (int i = 0; i < NV; ++i) acc = __builtin_fmaf(v[i], v[i], acc);
+    var = L::sum(acc, red + kWaves) / kf;  // slot 1
   }
-  inv = 1.0f / sqrtf(var + eps);
+  return 1.0f / sqrtf(var + eps);
 }
 
-// Modulation of 8 values of chunk j, then the O(...) cast.
-template <int PDT>
-__device__ __forceinline__ void modulate8(const PrepParams& p, int64_t row, int64_t j, float mean, float inv,
-                                          int round_dt, float (&v)[8]) {
-  float g[8], sc[8], sh[8];
-  const int64_t toff = p.row_map ? static_cast<int64_t>(p.row_map[row]) * p.k : 0;
-  load8<PDT>(p.gamma, j, g);
-  load8<PDT>(p.scale, toff + j, sc);
-  load8<PDT>(p.shift, toff + j, sh);
+// Raw 16-byte words of 8 elements of dtype DT (one word for 2-byte types, two for FP32).
+template <int DT>
+struct Raw8 {
+  uint4 w[dtype_bytes<DT>() / 2];
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> fetch8(const void* base, int64_t e) {
+  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) + e * dtype_bytes<DT>());
+  Raw8<DT> r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float normalized = (v[i] - mean) * inv * g[i];
-    const float modulated = normalized * (1.0f + sc[i]) + sh[i];
-    v[i] = round_dt == M5K_BF16 ? round_through<M5K_BF16>(modulated)
-           : round_dt == M5K_F16 ? round_through<M5K_F16>(modulated)
-                                 : modulated;
-  }
+  for (int i = 0; i < dtype_bytes<DT>() / 2; ++i) r.w[i] = p[i];
+  return r;
 }
 
-// Fused kernel.  CPT chunks of EPC elements per lane.
-template <int XDT, int PDT, int B, int CPT, bool GATED>
-__global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p) {
-  __shared__ float red[kWaves];
-  constexpr int EPC = Shape<B>::EPC;
-  constexpr int NV = CPT * EPC;
-  const int64_t row = blockIdx.x;
-  const int64_t nchunks = p.k / EPC;
-  float v[NV];
-  bool live[NV / 8];
+template <int DT>
+__device__ __forceinline__ void decode8(const Raw8<DT>& r, float (&v)[8]) {
+  if constexpr (DT == M5K_F32) {
+    const uint32_t w[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+  } else {
+    const uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
 #pragma unroll
-    for (int h = 0; h < EPC / 8; ++h) {
-      float t[8];
-      live[i * (EPC / 8) + h] = c < nchunks;
-      if (c < nchunks) {
-        load_row_chunk<XDT, PDT, GATED>(p, row, c * EPC + 8 * h, t);
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == M5K_BF16) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
       } else {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) t[r] = 0.0f;
+        v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
       }
-#pragma unroll
-      for (int r = 0; r < 8; ++r) v[i * EPC + 8 * h + r] = t[r];
     }
   }
-  float mean, inv;
-  row_stats<NV>(v, live, p.k, p.layer, p.eps, red, mean, inv);
-  const int round_dt = p.round_input ? XDT : M5K_F32;
+}
+
+// Fused kernel: NCH chunks of EPC elements per lane under layout L.  Every global load of
+// the row (X, branch, gate, gamma, scale, shift, signs) is issued up front, so a row waits
+// for memory once.
+template <class L, int XDT, int PDT, int B, int NCH, bool GATED>
+__global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int64_t rows) {
+  __shared__ float red[3 * kWaves];  // one slot per block reduction
+  constexpr int EPC = Shape<B>::EPC;
+  constexpr int NV = NCH * EPC;
+  constexpr int N8 = NV / 8;  // 8-element groups per lane
+  const int64_t row = L::row();
+  const int lane = L::lane();
+  const int64_t nchunks = p.k / EPC;
+  const int64_t goff = GATED && p.gate_map ? static_cast<int64_t>(p.gate_map[row]) * p.k : 0;
+  const int64_t toff = p.row_map ? static_cast<int64_t>(p.row_map[row]) * p.k : 0;
+  bool live[N8];
+  Raw8<XDT> xr[N8];
+  Raw8<XDT> br[GATED ? N8 : 1];
+  Raw8<PDT> gr[GATED ? N8 : 1], gam[N8], scl[N8], shf[N8];
+  uint2 sgn[N8];
+#pragma unroll
+  for (int g = 0; g < N8; ++g) {
+    const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * L::kLanes;
+    const int64_t j = c * EPC + 8 * (g % (EPC / 8));
+    live[g] = c < nchunks;
+    if (live[g]) {
+      xr[g] = fetch8<XDT>(p.x, row * p.k + j);
+      if constexpr (GATED) {
+        br[g] = fetch8<XDT>(p.branch, row * p.k + j);
+        gr[g] = fetch8<PDT>(p.gate, goff + j);
+      }
+      gam[g] = fetch8<PDT>(p.gamma, j);
+      scl[g] = fetch8<PDT>(p.scale, toff + j);
+      shf[g] = fetch8<PDT>(p.shift, toff + j);
+      sgn[g] = *reinterpret_cast<const uint2*>(p.signs + j);
+    }
+  }
+  float v[NV];
+#pragma unroll
+  for (int g = 0; g < N8; ++g) {
+    const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * L::kLanes;
+    const int64_t j = c * EPC + 8 * (g % (EPC / 8));
+    float t[8];
+    if (live[g]) {
+      decode8<XDT>(xr[g], t);
+      if constexpr (GATED) {
+        float b[8], gt[8];
+        decode8<XDT>(br[g], b);
+        decode8<PDT>(gr[g], gt);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = t[i] + b[i] * gt[i];
+        uint32_t w[8 * dtype_bytes<XDT>() / 4];
+        round8<XDT>(t, w);
+        store_words8<XDT>(p.r_next, row * p.k + j, w);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[8 * g + i] = t[i];
+  }
+  const float inv = row_stats<L, NV>(v, live, p.k, p.layer, p.eps, red);
   float peak = 0.0f;
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+  for (int ci = 0; ci < NCH; ++ci) {
     float z[EPC];
 #pragma unroll
     for (int h = 0; h < EPC / 8; ++h) {
+      const int g = ci * (EPC / 8) + h;
       float t[8];
+      if (live[g]) {
+        float gm[8], sc[8], sh[8];
+        decode8<PDT>(gam[g], gm);
+        decode8<PDT>(scl[g], sc);
+        decode8<PDT>(shf[g], sh);
 #pragma unroll
-      for (int r = 0; r < 8; ++r) t[r] = v[i * EPC + 8 * h + r];
-      if (c < nchunks) {
-        const int64_t j = c * EPC + 8 * h;
-        modulate8<PDT>(p, row, j, mean, inv, round_dt, t);
-        const uint2 sg = *reinterpret_cast<const uint2*>(p.signs + j);
+        for (int i = 0; i < 8; ++i) t[i] = __builtin_fmaf(v[8 * g + i] * inv * gm[i], 1.0f + sc[i], sh[i]);
+        if (p.round_input) {
+          uint32_t w[8 * dtype_bytes<XDT>() / 4];
+          round8<XDT>(t, w);
+        }
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const uint32_t byte = ((r < 4 ? sg.x : sg.y) >> (8 * (r & 3))) & 0xFFu;
-          t[r] = t[r] * static_cast<float>(static_cast<int8_t>(byte));
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t byte = ((i < 4 ? sgn[g].x : sgn[g].y) >> (8 * (i & 3))) & 0xFFu;
+          t[i] = t[i] * static_cast<float>(static_cast<int8_t>(byte));
         }
       } else {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) t[r] = 0.0f;
+        for (int i = 0; i < 8; ++i) t[i] = 0.0f;
       }
 #pragma unroll
-      for (int r = 0; r < 8; ++r) z[8 * h + r] = t[r];
+      for (int i = 0; i < 8; ++i) z[8 * h + i] = t[i];
     }
     hadamard::butterflies<B>(z);
 #pragma unroll
     for (int r = 0; r < EPC; ++r) {
-      v[i * EPC + r] = z[r];
+      v[ci * EPC + r] = z[r];
       peak = fmaxf(peak, fabsf(z[r]));
     }
   }
-  peak = block_max<kWaves>(peak, red);
+  peak = L::max(peak, red + 2 * kWaves);  // slot 2
   const I8Scale enc = i8_scale(quant_scale<M5K_QUANT_INT8>(peak));
-  if (threadIdx.x == 0) p.scales[row] = enc.scale;
+  if (lane == 0) p.scales[row] = enc.scale;
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
-    if (c < nchunks) {
-      uint2* out = reinterpret_cast<uint2*>(p.q + row * p.k + c * EPC);
+  for (int g = 0; g < N8; ++g) {
+    if (live[g]) {
+      const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * L::kLanes;
+      const int64_t j = c * EPC + 8 * (g % (EPC / 8));
+      float t[8];
 #pragma unroll
-      for (int t = 0; t < EPC / 8; ++t) {
-        float g[8];
-#pragma unroll
-        for (int b = 0; b < 8; ++b) g[b] = v[i * EPC + 8 * t + b];
-        uint32_t w[2];
-        encode_i8<8>(g, enc, w);
-        out[t] = make_uint2(w[0], w[1]);
-      }
+      for (int i = 0; i < 8; ++i) t[i] = v[8 * g + i];
+      uint32_t w[2];
+      encode_i8<8>(t, enc, w);
+      *reinterpret_cast<uint2*>(p.q + row * p.k + j) = make_uint2(w[0], w[1]);
     }
   }
 }
 
-// Staged norm + modulation (norm_modulate.metal): the fused kernel's EPC = 8 chunking and
-// reduction tree, output in the round dtype.
-template <int XDT, int PDT, int CPT>
-__global__ __launch_bounds__(kThreads) void norm_modulate_kernel(PrepParams p) {
-  __shared__ float red[kWaves];
-  constexpr int NV = CPT * 8;
-  const int64_t row = blockIdx.x;
-  const int64_t nchunks = p.k / 8;
-  float v[NV];
-  bool live[CPT];
+// Modulation of 8 centred values at column j, as in fused_prep_kernel:
+// fma((c * inv) * gamma, 1 + scale, shift).
+template <int PDT>
+__device__ __forceinline__ void modulate8(const PrepParams& p, int64_t toff, int64_t j, float inv, float (&v)[8]) {
+  float g[8], sc[8], sh[8];
+  load8<PDT>(p.gamma, j, g);
+  load8<PDT>(p.scale, toff + j, sc);
+  load8<PDT>(p.shift, toff + j, sh);
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+  for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(v[i] * inv * g[i], 1.0f + sc[i], sh[i]);
+}
+
+// Staged norm + modulation (norm_modulate.metal): the fused kernel's chunking (EPC = 8),
+// layout and reduction tree, output in the round dtype.
+template <class L, int XDT, int PDT, int NCH>
+__global__ __launch_bounds__(kThreads) void norm_modulate_kernel(PrepParams p, int64_t rows) {
+  __shared__ float red[2 * kWaves];  // one slot per block reduction
+  constexpr int NV = NCH * 8;
+  const int64_t row = L::row();
+  const int lane = L::lane();
+  const int64_t nchunks = p.k / 8;
+  const int64_t toff = p.row_map ? static_cast<int64_t>(p.row_map[row]) * p.k : 0;
+  float v[NV];
+  bool live[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = lane + static_cast<int64_t>(i) * L::kLanes;
     float t[8];
     live[i] = c < nchunks;
     if (c < nchunks) {
@@ -255,19 +368,24 @@ __global__ __launch_bounds__(kThreads) void norm_modulate_kernel(PrepParams p) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) v[8 * i + r] = t[r];
   }
-  float mean, inv;
-  row_stats<NV>(v, live, p.k, p.layer, p.eps, red, mean, inv);
-  const int round_dt = p.round_input ? XDT : M5K_F32;
+  const float inv = row_stats<L, NV>(v, live, p.k, p.layer, p.eps, red);
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = lane + static_cast<int64_t>(i) * L::kLanes;
     if (c < nchunks) {
       float t[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) t[r] = v[8 * i + r];
-      modulate8<PDT>(p, row, c * 8, mean, inv, round_dt, t);
-      if (p.round_input) store8<XDT>(p.y, row * p.k + c * 8, t);
-      else store8<M5K_F32>(p.y, row * p.k + c * 8, t);
+      modulate8<PDT>(p, toff, c * 8, inv, t);
+      if (p.round_input) {
+        uint32_t w[8 * dtype_bytes<XDT>() / 4];
+        round8<XDT>(t, w);
+        store_words8<XDT>(p.y, row * p.k + c * 8, w);
+      } else {
+        uint32_t w[8];
+        round8<M5K_F32>(t, w);
+        store_words8<M5K_F32>(p.y, row * p.k + c * 8, w);
+      }
     }
   }
 }
@@ -279,21 +397,24 @@ __global__ __launch_bounds__(kThreads) void gated_residual_kernel(PrepParams p, 
   if (c >= total_chunks) return;
   const int64_t e = c * 8;
   const int64_t row = e / p.k, j = e - row * p.k;
+  const int64_t goff = p.gate_map ? static_cast<int64_t>(p.gate_map[row]) * p.k : 0;
   float v[8];
-  load_row_chunk<XDT, PDT, true>(p, row, j, v);  // writes R_next
+  load_input8<XDT, PDT, true>(p, row, goff, j, v);  // writes R_next
 }
 
 template <int XDT, int PDT, int B, bool GATED>
 int launch_fused(const PrepParams& p, int64_t rows, hipStream_t st) {
-  const int64_t per_thread = (p.k / Shape<B>::EPC + kThreads - 1) / kThreads;
-  const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
-  if (per_thread <= 1) fused_prep_kernel<XDT, PDT, B, 1, GATED><<<grid, block, 0, st>>>(p);
-  else if (per_thread <= 2) fused_prep_kernel<XDT, PDT, B, 2, GATED><<<grid, block, 0, st>>>(p);
-  else if (per_thread <= 4) fused_prep_kernel<XDT, PDT, B, 4, GATED><<<grid, block, 0, st>>>(p);
-  else if (per_thread <= 8) fused_prep_kernel<XDT, PDT, B, 8, GATED><<<grid, block, 0, st>>>(p);
+  constexpr int EPC = Shape<B>::EPC;
+  const dim3 block(kThreads);
+  const int64_t per_thread = (p.k / EPC + kThreads - 1) / kThreads;
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (per_thread <= 1) fused_prep_kernel<GroupRow, XDT, PDT, B, 1, GATED><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 2) fused_prep_kernel<GroupRow, XDT, PDT, B, 2, GATED><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 4) fused_prep_kernel<GroupRow, XDT, PDT, B, 4, GATED><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 8) fused_prep_kernel<GroupRow, XDT, PDT, B, 8, GATED><<<grid, block, 0, st>>>(p, rows);
   else {
     set_error("m5k_norm_hadamard_quantize: K=%lld exceeds the register-resident row limit %d", (long long)p.k,
-              8 * kThreads * Shape<B>::EPC);
+              8 * kThreads * EPC);
     return M5K_EINVAL;
   }
   return launch_status("m5k_norm_hadamard_quantize");
@@ -326,12 +447,13 @@ int fused_by_param(int pdt, int block, const PrepParams& p, int64_t rows, hipStr
 
 template <int XDT, int PDT>
 int launch_norm(const PrepParams& p, int64_t rows, hipStream_t st) {
+  const dim3 block(kThreads);
   const int64_t per_thread = (p.k / 8 + kThreads - 1) / kThreads;
-  const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
-  if (per_thread <= 1) norm_modulate_kernel<XDT, PDT, 1><<<grid, block, 0, st>>>(p);
-  else if (per_thread <= 2) norm_modulate_kernel<XDT, PDT, 2><<<grid, block, 0, st>>>(p);
-  else if (per_thread <= 4) norm_modulate_kernel<XDT, PDT, 4><<<grid, block, 0, st>>>(p);
-  else if (per_thread <= 8) norm_modulate_kernel<XDT, PDT, 8><<<grid, block, 0, st>>>(p);
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (per_thread <= 1) norm_modulate_kernel<GroupRow, XDT, PDT, 1><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 2) norm_modulate_kernel<GroupRow, XDT, PDT, 2><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 4) norm_modulate_kernel<GroupRow, XDT, PDT, 4><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 8) norm_modulate_kernel<GroupRow, XDT, PDT, 8><<<grid, block, 0, st>>>(p, rows);
   else {
     set_error("m5k_norm_modulate: K=%lld exceeds the register-resident row limit %d", (long long)p.k, 8 * kThreads * 8);
     return M5K_EINVAL;
