@@ -75,11 +75,94 @@ __device__ __forceinline__ void norm_rope_16(const float (&z)[8], Partner partne
   *reinterpret_cast<uint4*>(out) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
 }
 
+// Fast path for rope_half % 8 == 0 (R = 48 and 64 included): a lane's 8 channels are either
+// all rotated-lower (d < R), all rotated-upper (R <= d < 2R) or all unrotated, the partner of
+// channel d lives on lane lg +- R/8 at the same register index, and cos/sin of the lane's
+// channels are 8 consecutive BF16 values (one 16-byte load each).  u[d] is computed once by
+// its owner and fetched by the partner lane: the same FP32 expression as norm_rope_16, so the
+// two paths give identical bits.
+struct LaneRope {
+  float gam[8];  // gamma of the lane's channels
+  int src;       // partner lane within the 16-lane group
+  bool rot, lower;
+};
+
+__device__ __forceinline__ LaneRope lane_rope(const QkParams& p, int lg) {
+  LaneRope r;
+  const uint4 g = *reinterpret_cast<const uint4*>(p.gamma + 8 * lg);
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    r.gam[2 * t] = __uint_as_float(gw[t] << 16);
+    r.gam[2 * t + 1] = __uint_as_float(gw[t] & 0xFFFF0000u);
+  }
+  const int R = p.rope_half, d0 = 8 * lg;
+  r.rot = d0 < 2 * R;
+  r.lower = d0 < R;
+  r.src = !r.rot ? lg : r.lower ? lg + R / 8 : lg - R / 8;
+  return r;
+}
+
+// cos and sin of the lane's 8 channels for `row` (zeros for unrotated lanes).
+__device__ __forceinline__ void lane_cos_sin(const QkParams& p, const LaneRope& r, int64_t row, int lg, uint4& c,
+                                             uint4& s) {
+  if (r.rot) {
+    const int j0 = r.lower ? 8 * lg : 8 * lg - p.rope_half;
+    const int64_t off = row * p.rope_half + j0;
+    c = *reinterpret_cast<const uint4*>(p.cos + off);
+    s = *reinterpret_cast<const uint4*>(p.sin + off);
+  } else {
+    c = make_uint4(0, 0, 0, 0);
+    s = make_uint4(0, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void unpack8_bf16(const uint4& w, float (&v)[8]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    v[2 * t] = __uint_as_float(ws[t] << 16);
+    v[2 * t + 1] = __uint_as_float(ws[t] & 0xFFFF0000u);
+  }
+}
+
+// Normalize + rotate one (row, head) held as z[8] per lane; returns the packed BF16 output.
+__device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneRope& r, const uint4& cw,
+                                                const uint4& sw, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ss += z[t] * z[t];
+  ss += __shfl_xor(ss, 1, 16);
+  ss += __shfl_xor(ss, 2, 16);
+  ss += __shfl_xor(ss, 4, 16);
+  ss += __shfl_xor(ss, 8, 16);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(HEAD) + eps);
+  float u[8], c[8], s[8];
+  unpack8_bf16(cw, c);
+  unpack8_bf16(sw, s);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) u[t] = (z[t] * inv) * r.gam[t];
+  uint32_t packed[4];
+#pragma unroll
+  for (int t = 0; t < 8; t += 2) {
+    float y[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float pu = __shfl(u[t + e], r.src, 16);
+      const float a = u[t + e] * c[t + e], b = pu * s[t + e];
+      y[e] = !r.rot ? u[t + e] : r.lower ? a - b : a + b;
+    }
+    packed[t / 2] = f32x2_to_bf16x2(y[0], y[1]);
+  }
+  return make_uint4(packed[0], packed[1], packed[2], packed[3]);
+}
+
 template <int MODE, bool ALIGNED>
 __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const uint8_t* __restrict__ A,
                                                                           const uint8_t* __restrict__ B, int M, int N,
                                                                           int64_t Kb, const float* __restrict__ sa,
-                                                                          const float* __restrict__ sb, QkParams p) {
+                                                                          const float* __restrict__ sb, QkParams p,
+                                                                          int fast) {
   using G = KernelGrid;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
@@ -88,6 +171,23 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   AccTile<MODE, G> acc;
   if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+
+  const int group = threadIdx.x >> 4, lg = threadIdx.x & 15;
+  constexpr int GROUPS = G::THREADS / 16;  // 32 groups of 16 lanes
+  constexpr int ROWS_PER_GROUP = BM / GROUPS;
+  const int heads_here = (N - n0) >= BN ? 2 : 1;  // N is a multiple of 128
+
+  // Fast path: issue the per-row cos/sin loads of this group's rows before staging the tile.
+  LaneRope lr;
+  uint4 cw[ROWS_PER_GROUP], sw[ROWS_PER_GROUP];
+  if (fast) {
+    lr = lane_rope(p, lg);
+#pragma unroll
+    for (int i = 0; i < ROWS_PER_GROUP; ++i) {
+      const int row = m0 + group + GROUPS * i;
+      if (row < M) lane_cos_sin(p, lr, row, lg, cw[i], sw[i]);
+    }
+  }
 
   // BF16 projection tile [256 rows][256 cols] in LDS (row stride 512 B).  The main loop ended
   // with a drained DMA and a barrier, so the stage ring is free.
@@ -100,22 +200,33 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   });
   __syncthreads();
 
-  const int group = threadIdx.x >> 4, lg = threadIdx.x & 15;
-  constexpr int GROUPS = G::THREADS / 16;
+  if (fast) {
+#pragma unroll
+    for (int i = 0; i < ROWS_PER_GROUP; ++i) {
+      const int local_row = group + GROUPS * i;
+      const int row = m0 + local_row;
+      if (row >= M) continue;  // uniform across the 16-lane group
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h >= heads_here) continue;
+        const uint16_t* src = tile + local_row * BN + h * HEAD;
+        float z[8];
+        unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
+        const uint4 out = norm_rope_fast(z, lr, cw[i], sw[i], p.eps);
+        const int head = n0 / HEAD + h;
+        *reinterpret_cast<uint4*>(p.y + (static_cast<int64_t>(head) * M + row) * HEAD + 8 * lg) = out;
+      }
+    }
+    return;
+  }
   for (int q = group; q < BM * 2; q += GROUPS) {
     const int local_row = q >> 1, local_head = q & 1;
     const int row = m0 + local_row;
     const int head = n0 / HEAD + local_head;
     if (row >= M || head * HEAD >= N) continue;  // uniform across the 16-lane group
     const uint16_t* src = tile + local_row * BN + local_head * HEAD;
-    const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     float z[8];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      z[2 * t] = bf16_bits_to_f32(ws[t] & 0xFFFFu);
-      z[2 * t + 1] = bf16_bits_to_f32(ws[t] >> 16);
-    }
+    unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
     norm_rope_16(z, [&](int d) { return bf16_bits_to_f32(src[d]); }, p, row, M, head, lg);
   }
 }
@@ -123,7 +234,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
 // Staged postprocess of a BF16 [M, N] projection: one 16-lane group per (row, head), consecutive
 // groups walking the heads of a row (coalesced 256-byte reads).
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __restrict__ P, int64_t M, int64_t N,
-                                                           QkParams p) {
+                                                           QkParams p, int fast) {
   const int64_t heads = N / HEAD;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
   const int lg = threadIdx.x & 15;
@@ -131,15 +242,22 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
   const int64_t row = q / heads;
   const int head = static_cast<int>(q - row * heads);
   const uint16_t* src = P + row * N + static_cast<int64_t>(head) * HEAD;
-  const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
   float z[8];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    z[2 * t] = bf16_bits_to_f32(ws[t] & 0xFFFFu);
-    z[2 * t + 1] = bf16_bits_to_f32(ws[t] >> 16);
+  unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
+  if (fast) {
+    const LaneRope lr = lane_rope(p, lg);
+    uint4 cw, sw;
+    lane_cos_sin(p, lr, row, lg, cw, sw);
+    const uint4 out = norm_rope_fast(z, lr, cw, sw, p.eps);
+    *reinterpret_cast<uint4*>(p.y + (static_cast<int64_t>(head) * M + row) * HEAD + 8 * lg) = out;
+    return;
   }
   norm_rope_16(z, [&](int d) { return bf16_bits_to_f32(src[d]); }, p, row, M, head, lg);
+}
+
+// The fast path needs whole 8-channel lanes per RoPE half and 16-byte aligned tables.
+inline int fast_rope(const QkParams& p) {
+  return p.rope_half % 8 == 0 && aligned16(p.gamma) && (p.rope_half == 0 || (aligned16(p.cos) && aligned16(p.sin)));
 }
 
 template <int MODE>
@@ -152,8 +270,9 @@ int launch_fused(const void* a, const void* b, int64_t m, int64_t n, int64_t k, 
   const dim3 grid(static_cast<unsigned>(tiles)), block(KernelGrid::THREADS);
   auto* A = static_cast<const uint8_t*>(a);
   auto* B = static_cast<const uint8_t*>(b);
-  if (aligned) qk_fused_kernel<MODE, true><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p);
-  else qk_fused_kernel<MODE, false><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p);
+  const int fast = fast_rope(p);
+  if (aligned) qk_fused_kernel<MODE, true><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p, fast);
+  else qk_fused_kernel<MODE, false><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p, fast);
   return launch_status("m5k_projection_qk_rope");
 }
 
@@ -207,6 +326,6 @@ extern "C" int m5k_qk_norm_rope(const void* projected, int64_t m, int64_t n, con
   const int64_t blocks = (groups + 15) / 16;
   M5K_REQUIRE(blocks <= 0x7FFFFFFF, "%s: input too large", name);
   qk_norm_rope_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream)>>>(
-      static_cast<const uint16_t*>(projected), m, n, p);
+      static_cast<const uint16_t*>(projected), m, n, p, fast_rope(p));
   return launch_status(name);
 }
