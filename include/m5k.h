@@ -14,7 +14,7 @@
  * ValueError / NotImplementedError contract before calling in.
  *
  * Reference interfaces replaced (paths relative to the reference repository):
- *   quantize                 src/m5kernels/metal.py:27-44
+ *   quantize                 src/m5kernels/metal.py:27-44 (int8, fp8, mxint8)
  *   gemm                     src/m5kernels/metal.py:158-269
  *   rotate                   src/m5kernels/hadamard.py:33-77
  *   fused_norm_hadamard_quantize
@@ -73,6 +73,25 @@ int m5k_abi_version(void);
  */
 int m5k_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int mode,
                       void* q, float* scales, void* stream);
+
+/*
+ * MXINT8 block quantizer.  Replaces metal.quantize(x, "mxint8") (src/m5kernels/metal.py:27-44,
+ * block mode of shaders/quantize.metal:13-37; spec numerics.py:33-41).  x: [rows,k] F32/F16/BF16
+ * with k % 32 == 0.  Per 32-element block: e = 0 for an all-zero block, else
+ * clamp(floor(log2(peak)) - 6, -127, 127) with log2 rounded to FP32 before the floor;
+ * q = clamp(rint(x / 2^e), -127, 127) int8 [rows,k]; exponents[rows, k/32] = e + 127 (uint8,
+ * the E8M0 scale byte of the OCP S1.6 convention with the /64 folded in).
+ */
+int m5k_quantize_mxint8(const void* x, int x_dtype, int64_t rows, int64_t k, int8_t* q,
+                        uint8_t* exponents, void* stream);
+
+/*
+ * MXINT8 codes to BF16 values q * 2^(exponent - 127), exact.  Operand expansion for the MXINT8
+ * linear (metal.gemm(..., "mxint8", ...), src/m5kernels/metal.py:81-86, plane scales of
+ * 32 x 1 blocks): y[rows,k] BF16, 16-byte aligned; q 8-byte aligned; k % 32 == 0.
+ */
+int m5k_mxint8_to_bf16(const int8_t* q, const uint8_t* exponents, int64_t rows, int64_t k, void* y,
+                       void* stream);
 
 /*
  * W8A8 linear.  Replaces metal.gemm(a, b, "int8", ...) (src/m5kernels/metal.py:158-269,

@@ -9,7 +9,8 @@
 // rows are 64 B with the 16-byte chunk index XOR-swizzled by (row >> 2) & 3 (see swz()).
 //
 // MFMA operand layout (32 x 32 blocks): lane l supplies row (l & 31) and a 16-byte
-// (32-byte for FP8) slice of K selected by (l >> 5).  A and B use the same K-slice
+// (32-byte for FP8) slice of K selected by (l >> 5); FP32 issues one K = 2 MFMA per float
+// of the slice.  A and B use the same K-slice
 // mapping, so the products pair up correctly whatever order the hardware sums them in
 // (exact for INT32 accumulation).  Accumulator register r of lane l holds
 // C[(r >> 2) * 8 + (l >> 5) * 4 + (r & 3)][l & 31].
@@ -29,7 +30,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-enum Mode { I8 = 0, F8 = 1, BF16 = 2, F16 = 3 };
+enum Mode { I8 = 0, F8 = 1, BF16 = 2, F16 = 3, F32 = 4 };
 
 constexpr int BM = 256;   // tile rows (A rows / C rows)
 constexpr int BN = 256;   // tile cols (B rows / C cols)
@@ -68,6 +69,12 @@ struct Traits<I8> {
   static constexpr int sub_steps = BKB / 32;
 };
 template <>
+struct Traits<F32> {
+  using acc_t = v16f;
+  static constexpr int elem_bytes = 4;
+  static constexpr int sub_steps = BKB / 32;  // 8 floats of K per sub-step, 4 MFMAs of K = 2
+};
+template <>
 struct Traits<F8> {
   using acc_t = v16f;
   static constexpr int elem_bytes = 1;
@@ -92,6 +99,12 @@ __device__ __forceinline__ void mfma(typename Traits<MODE>::acc_t& acc, const Fr
   } else if constexpr (MODE == F16) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a.lo),
                                                  __builtin_bit_cast(f16x8, b.lo), acc, 0, 0, 0);
+  } else if constexpr (MODE == F32) {
+    // A 16-byte fragment holds 4 consecutive floats of K; MFMA j takes float j of every lane,
+    // so lanes l and l + 32 contribute K offsets j and 4 + j of the 8-float sub-step.
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__int_as_float(a.lo[j]), __int_as_float(b.lo[j]), acc, 0, 0, 0);
   } else {
     const v8i av = {a.lo[0], a.lo[1], a.lo[2], a.lo[3], a.hi[0], a.hi[1], a.hi[2], a.hi[3]};
     const v8i bv = {b.lo[0], b.lo[1], b.lo[2], b.lo[3], b.hi[0], b.hi[1], b.hi[2], b.hi[3]};

@@ -1,4 +1,4 @@
-// C-ABI entry point of the BF16/FP16 linear (FP32 accumulation); kernels in gemm_launch.h.
+// C-ABI entry point of the BF16/FP16/FP32 linear (FP32 accumulation); kernels in gemm_launch.h.
 #include "gemm_launch.h"
 
 using namespace m5k;
@@ -24,6 +24,13 @@ extern "C" int m5k_gemm_float(const void* a, const void* b, int ab_dtype, int64_
       case M5K_BF16: return launch_plain<BF16, M5K_BF16>(a, b, m, n, k, p, st, name);
       case M5K_F16: return launch_plain<BF16, M5K_F16>(a, b, m, n, k, p, st, name);
       case M5K_F32: return launch_plain<BF16, M5K_F32>(a, b, m, n, k, p, st, name);
+      default: break;
+    }
+  } else if (ab_dtype == M5K_F32 && !residual) {
+    switch (c_dtype) {
+      case M5K_BF16: return launch<F32, M5K_BF16, EPI_NONE, EPI_NONE, false>(a, b, m, n, k, p, st, name);
+      case M5K_F16: return launch<F32, M5K_F16, EPI_NONE, EPI_NONE, false>(a, b, m, n, k, p, st, name);
+      case M5K_F32: return launch<F32, M5K_F32, EPI_NONE, EPI_NONE, false>(a, b, m, n, k, p, st, name);
       default: break;
     }
   } else if (ab_dtype == M5K_F16) {

@@ -178,6 +178,75 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_scalar(const void* __r
     q[base + j] = static_cast<uint8_t>(quant_encode<MODE>(load_elem<DT>(x, base + j), scale));
 }
 
+// ---- MXINT8 (32-element blocks with a shared power-of-two scale) ----------------------------
+// numerics.py:33-41 and quantize.metal's block mode: per block, e = 0 for an all-zero block,
+// else clamp(floor(log2(peak)) - 6, -127, 127) with log2 rounded to FP32 before the floor (a
+// peak just below 2^k gives k, as the reference's float32 log2 does); code =
+// clamp(rint(x / 2^e), -127, 127); exponent byte e + 127.  Four lanes own a block, 8 elements
+// each; the quad reduces its peak with DPP.  Division by 2^e is exact scaling, so
+// ldexp(x, -e) rounds to the same value.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void quantize_mx_kernel(const uint8_t* __restrict__ x, int64_t blocks,
+                                                               int8_t* __restrict__ q, uint8_t* __restrict__ s) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if ((t >> 2) >= blocks) return;  // whole quads leave together
+  constexpr int EB = dtype_bytes<DT>();
+  const uint4* p = reinterpret_cast<const uint4*>(x + t * 8 * EB);
+  float v[8];
+  if constexpr (DT == M5K_F32) {
+    const uint4 a = p[0], b = p[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+  } else {
+    const uint4 a = p[0];
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = half_to_f32<DT>(w[i] & 0xFFFFu);
+      v[2 * i + 1] = half_to_f32<DT>(w[i] >> 16);
+    }
+  }
+  float peak = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) peak = fmaxf(peak, fabsf(v[i]));
+  peak = fmaxf(peak, dpp_move<0xB1>(peak));  // quad_perm [1,0,3,2]
+  peak = fmaxf(peak, dpp_move<0x4E>(peak));  // quad_perm [2,3,0,1]
+  int e = 0;
+  if (peak > 0.0f) {
+    const float l = static_cast<float>(log2(static_cast<double>(peak)));
+    e = min(max(static_cast<int>(floorf(l)) - 6, -127), 127);
+  }
+  uint32_t code[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) code[i] = i8_clamp_code(rintf(ldexpf(v[i], -e)));
+  *reinterpret_cast<uint2*>(q + t * 8) =
+      make_uint2(code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
+                 code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24));
+  if ((t & 3) == 0) s[t >> 2] = static_cast<uint8_t>(e + 127);
+}
+
+// MXINT8 codes to BF16 values code * 2^(e - 127): exact (|code| <= 127 fits the BF16
+// significand), 8 elements per thread.
+__global__ __launch_bounds__(kThreads) void mx_to_bf16_kernel(const int8_t* __restrict__ q,
+                                                              const uint8_t* __restrict__ s, int64_t groups,
+                                                              uint16_t* __restrict__ y) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= groups) return;
+  const uint2 w = *reinterpret_cast<const uint2*>(q + t * 8);
+  const int e = static_cast<int>(s[t >> 2]) - 127;
+  uint32_t out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t word = i < 2 ? w.x : w.y;
+    const int sh = 16 * (i & 1);
+    const float lo = ldexpf(static_cast<float>(static_cast<int8_t>((word >> sh) & 0xFFu)), e);
+    const float hi = ldexpf(static_cast<float>(static_cast<int8_t>((word >> (sh + 8)) & 0xFFu)), e);
+    out[i] = f32x2_to_bf16x2(lo, hi);
+  }
+  *reinterpret_cast<uint4*>(y + t * 8) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
 template <int DT, int MODE, int CPT>
 void launch_vec(const uint8_t* x, int64_t rows, int64_t k, uint8_t* q, float* s, hipStream_t st) {
   quantize_rows_vec<DT, MODE, CPT><<<dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st>>>(x, k, q, s);
@@ -225,4 +294,45 @@ extern "C" int m5k_quantize_rows(const void* x, int x_dtype, int64_t rows, int64
     case M5K_F32: return dispatch_mode<M5K_F32>(mode, x, rows, k, q, scales, st);
     default: set_error("m5k_quantize_rows: unsupported input dtype %d", x_dtype); return M5K_EINVAL;
   }
+}
+
+extern "C" int m5k_quantize_mxint8(const void* x, int x_dtype, int64_t rows, int64_t k, int8_t* q,
+                                   uint8_t* exponents, void* stream) {
+  using namespace m5k;
+  clear_error();
+  const char* name = "m5k_quantize_mxint8";
+  M5K_REQUIRE(x && q && exponents, "%s: null pointer", name);
+  M5K_REQUIRE(rows > 0 && k > 0 && k % 32 == 0, "%s: shape [%lld,%lld] needs K a positive multiple of 32", name,
+              (long long)rows, (long long)k);
+  M5K_REQUIRE(aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0, "%s: misaligned buffers", name);
+  const int64_t blocks = rows * (k / 32);
+  const int64_t groups = (blocks * 4 + kThreads - 1) / kThreads;
+  M5K_REQUIRE(groups <= 0x7FFFFFFF, "%s: input too large", name);
+  const dim3 grid(static_cast<unsigned>(groups)), block(kThreads);
+  hipStream_t st = as_stream(stream);
+  auto* xb = static_cast<const uint8_t*>(x);
+  switch (x_dtype) {
+    case M5K_BF16: quantize_mx_kernel<M5K_BF16><<<grid, block, 0, st>>>(xb, blocks, q, exponents); break;
+    case M5K_F16: quantize_mx_kernel<M5K_F16><<<grid, block, 0, st>>>(xb, blocks, q, exponents); break;
+    case M5K_F32: quantize_mx_kernel<M5K_F32><<<grid, block, 0, st>>>(xb, blocks, q, exponents); break;
+    default: set_error("%s: unsupported input dtype %d", name, x_dtype); return M5K_EINVAL;
+  }
+  return launch_status(name);
+}
+
+extern "C" int m5k_mxint8_to_bf16(const int8_t* q, const uint8_t* exponents, int64_t rows, int64_t k, void* y,
+                                  void* stream) {
+  using namespace m5k;
+  clear_error();
+  const char* name = "m5k_mxint8_to_bf16";
+  M5K_REQUIRE(q && exponents && y, "%s: null pointer", name);
+  M5K_REQUIRE(rows > 0 && k > 0 && k % 32 == 0, "%s: shape [%lld,%lld] needs K a positive multiple of 32", name,
+              (long long)rows, (long long)k);
+  M5K_REQUIRE((reinterpret_cast<uintptr_t>(q) & 7u) == 0 && aligned16(y), "%s: misaligned buffers", name);
+  const int64_t groups = rows * k / 8;
+  const int64_t blocks = (groups + kThreads - 1) / kThreads;
+  M5K_REQUIRE(blocks <= 0x7FFFFFFF, "%s: input too large", name);
+  mx_to_bf16_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, as_stream(stream)>>>(
+      q, exponents, groups, static_cast<uint16_t*>(y));
+  return launch_status(name);
 }

@@ -12,8 +12,8 @@ Differences that follow from the platform, not the contract:
   unpacked (so malformed tuples fail as in the reference) but the MI355X kernel
   always uses its own 256x256 MFMA tile with an XCD-aware raster.
 * ``tag`` only specialized the Metal kernel name; it is accepted and ignored.
-* ``mode="mxint8"`` and ``mode="fp32"`` are outside the MI355X hot path and raise
-  NotImplementedError.
+* ``mode="mxint8"`` GEMM expands both operands exactly to BF16 (codes times their block
+  scale) and runs the BF16 MFMA GEMM with FP32 accumulation.
 """
 
 from __future__ import annotations
@@ -40,13 +40,24 @@ def quantize(x, mode, tag="packed"):
 
     INT8: int8 codes in [-127, 127], scale = max|row| / 127 (1 for an all-zero row),
     code = rint_even(x / scale).  FP8: uint8 OCP E4M3 codes of x / scale with
-    scale = max|row| / 448.  Mirrors metal.quantize (metal.py:27-44).
+    scale = max|row| / 448.  MXINT8: int8 codes of 32-element blocks sharing a power-of-two
+    scale, returned as uint8 exponent bytes [rows, K/32] (e + 127, numerics.py:33-41).
+    Mirrors metal.quantize (metal.py:27-44).
     """
     rows, k = x.shape
     if mode == "mxint8":
         if k % 32:
             raise ValueError("MXINT8 requires K divisible by 32")
-        raise NotImplementedError("MXINT8 block quantization is not part of the MI355X hot path")
+        if x.dtype not in _FLOAT_DTYPES:
+            raise ValueError("quantization input must be float16, bfloat16 or float32")
+        if rows == 0:
+            raise ValueError("quantization input must be nonempty")
+        x = _lib.aligned_device_tensor(x, "x")
+        q = torch.empty((rows, k), dtype=torch.int8, device=x.device)
+        e = torch.empty((rows, k // 32), dtype=torch.uint8, device=x.device)
+        _lib.call("m5k_quantize_mxint8", _lib.ptr(x), _lib.dtype_code(x), rows, k, _lib.ptr(q), _lib.ptr(e),
+                  _lib.stream_of(x))
+        return q, e
     if mode not in _QUANT_MODES:
         raise ValueError(f"unknown quantization mode: {mode!r}")
     if x.dtype not in _FLOAT_DTYPES:
@@ -161,8 +172,8 @@ def gemm(
     if mode in {"int8", "fp8", "mxint8"}:
         if a_scales is None or b_scales is None:
             raise ValueError("scales required")
-    if mode in {"mxint8", "fp32"}:
-        raise NotImplementedError(f"{mode} GEMM is not part of the MI355X hot path")
+    if mode == "mxint8":
+        return _gemm_mxint8(a, b, a_scales, b_scales, output_dtype)
     if a.dtype != operand_dtype or b.dtype != operand_dtype:
         raise ValueError(f"{mode} GEMM requires {operand_dtype} operands")
     if m == 0 or n == 0 or k == 0:
@@ -237,6 +248,35 @@ def gemm(
             _lib.ptr(gate_row_map),
             stream,
         )
+    return c
+
+
+def _mx_to_bf16(q, e, name):
+    rows, k = q.shape
+    if q.dtype != torch.int8 or e.dtype != torch.uint8 or tuple(e.shape) != (rows, k // 32):
+        raise ValueError(f"MXINT8 {name} needs int8 codes [R,K] and uint8 exponents [R,K/32]")
+    q = _lib.device_tensor(q, name)
+    e = _lib.device_tensor(e, name + "_scales")
+    y = torch.empty((rows, k), dtype=torch.bfloat16, device=q.device)
+    _lib.call("m5k_mxint8_to_bf16", _lib.ptr(q), _lib.ptr(e), rows, k, _lib.ptr(y), _lib.stream_of(q))
+    return y
+
+
+def _gemm_mxint8(a, b, a_scales, b_scales, output_dtype):
+    """MXINT8 linear (metal.py:81-86 plane scales): C = sum over 32-wide K blocks of
+    2^(ea-127) 2^(eb-127) sum_k a b, FP32 accumulation.  Both operands expand exactly to BF16
+    (|code| <= 127 times a power of two) and run on the BF16 MFMA GEMM."""
+    m, k = a.shape
+    if k % 32:
+        raise ValueError("MXINT8 requires K divisible by 32")
+    out_dtype = output_dtype or torch.float32
+    if out_dtype not in _FLOAT_DTYPES:
+        raise ValueError("output_dtype must be float16, bfloat16 or float32")
+    ab = _mx_to_bf16(a, a_scales, "a")
+    bb = _mx_to_bf16(b, b_scales, "b")
+    c = torch.empty((m, b.shape[0]), dtype=out_dtype, device=ab.device)
+    _lib.call("m5k_gemm_float", _lib.ptr(ab), _lib.ptr(bb), _lib.BF16, m, b.shape[0], k, _lib.ptr(c),
+              _lib.dtype_code(c), None, None, None, _lib.stream_of(ab))
     return c
 
 

@@ -115,14 +115,33 @@ def fp8_encode(x) -> np.ndarray:
     return code | np.where(np.signbit(x), np.uint8(128), np.uint8(0))
 
 
-def quantize_reference(x, mode):
-    """Per-row symmetric quantizer in FP32 (numerics.py:29-46, modes int8 / fp8).
+def mx_exponent(peak):
+    """MXINT8 block exponent (numerics.py:36-38): floor of the FP32 log2 of the block peak, minus
+    6, clamped to [-127, 127]; 0 for an all-zero block.  The FP32 log2 rounds to nearest, so a
+    peak just below 2**k gives k (floor(log2) of the rounded value), as numpy's float32 log2 does."""
+    peak = np.asarray(peak, dtype=np.float32)
+    safe = np.maximum(peak, np.finfo(np.float32).tiny)
+    e = np.clip(np.floor(np.log2(safe.astype(np.float64)).astype(np.float32)) - 6, -127, 127)
+    return np.where(peak == 0, np.float32(0), e).astype(np.float32)
 
-    peak = max|x|; scale = 1 if peak == 0 else peak / 127 (or 448); z = x / scale;
-    int8 -> clip(rint(z), -127, 127); fp8 -> fp8_encode(z).  Rejects non-finite input."""
+
+def quantize_reference(x, mode):
+    """Quantizer in FP32 (numerics.py:29-46).
+
+    int8 / fp8: per row, peak = max|x|; scale = 1 if peak == 0 else peak / 127 (or 448);
+    z = x / scale; int8 -> clip(rint(z), -127, 127); fp8 -> fp8_encode(z).
+    mxint8: per 32-element block, e = mx_exponent(peak); codes clip(rint(x / 2**e), -127, 127);
+    scales uint8 e + 127 of shape [rows, K/32].  Rejects non-finite input."""
     x = np.asarray(x, dtype=np.float32)
     if not np.isfinite(x).all():
         raise ValueError("quantization input must be finite")
+    if mode == "mxint8":
+        if x.shape[-1] % 32:
+            raise ValueError("K must be divisible by 32")
+        z = x.reshape(*x.shape[:-1], -1, 32)
+        e = mx_exponent(np.max(np.abs(z), axis=-1, keepdims=True))
+        q = np.clip(np.rint(z / np.exp2(e)), -127, 127).astype(np.int8)
+        return q.reshape(x.shape), (e[..., 0] + 127).astype(np.uint8)
     if mode not in ("int8", "fp8"):
         raise ValueError(f"unsupported mode {mode!r}")
     peak = np.max(np.abs(x), axis=-1, keepdims=True)
@@ -137,7 +156,12 @@ def quantize_reference(x, mode):
 
 
 def dequantize(q, s, mode):
-    """Decoded FP32 values codes * row scale (numerics.py:49-54)."""
+    """Decoded FP32 values (numerics.py:49-54): codes * row scale, or for mxint8 codes * 2**(s - 127)
+    per 32-element block."""
+    if mode == "mxint8":
+        q = np.asarray(q)
+        z = q.reshape(*q.shape[:-1], -1, 32).astype(np.float32)
+        return (z * np.exp2(np.asarray(s).astype(np.int32) - 127).astype(np.float32)[..., None]).reshape(q.shape)
     z = fp8_decode(q) if mode == "fp8" else np.asarray(q).astype(np.float32)
     return z * np.asarray(s, dtype=np.float32)[..., None]
 

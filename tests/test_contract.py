@@ -16,7 +16,7 @@ def test_quantize_rejections():
         quantize(torch.zeros(2, 8), "int4")
     with pytest.raises(ValueError, match="MXINT8 requires K divisible by 32"):
         quantize(torch.zeros(2, 40), "mxint8")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="ROCm device"):  # mxint8 is computed, on the GPU only
         quantize(torch.zeros(2, 64), "mxint8")
     with pytest.raises(ValueError, match="float16, bfloat16 or float32"):
         quantize(torch.zeros(2, 8, dtype=torch.int8), "int8")
@@ -44,8 +44,14 @@ def test_gemm_shape_and_mode_rejections():
         gemm(_i8(2, 8), _i8(3, 8), "int8")
     with pytest.raises(KeyError):
         gemm(_i8(2, 8), _i8(3, 8), "int4")
-    with pytest.raises(NotImplementedError):
-        gemm(torch.zeros(2, 8), torch.zeros(3, 8), "fp32")
+    with pytest.raises(ValueError, match="divisible by 32"):
+        gemm(torch.zeros(2, 8, dtype=torch.int8), torch.zeros(3, 8, dtype=torch.int8), "mxint8",
+             a_scales=torch.zeros(2, 1, dtype=torch.uint8), b_scales=torch.zeros(3, 1, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="scales required"):
+        gemm(torch.zeros(2, 32, dtype=torch.int8), torch.zeros(3, 32, dtype=torch.int8), "mxint8")
+    with pytest.raises(ValueError, match="uint8 exponents"):
+        gemm(torch.zeros(2, 32, dtype=torch.int8), torch.zeros(3, 32, dtype=torch.int8), "mxint8",
+             a_scales=torch.zeros(2, dtype=torch.float32), b_scales=torch.zeros(3, 1, dtype=torch.uint8))
     with pytest.raises(ValueError):
         gemm(_i8(2, 8), _i8(3, 8), "int8", tile=(64, 64))
 

@@ -190,19 +190,35 @@ def test_fp8_ones_kat(kats, device):
     np.testing.assert_allclose(np_of(y), kat["expected"], rtol=1e-5)
 
 
-@pytest.mark.parametrize("mode", ["bf16", "fp16"])
-@pytest.mark.parametrize("shape", [(1, 33, 64), (127, 65, 96), (65, 17, 257), (300, 520, 1024)])
+@pytest.mark.parametrize("mode", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("shape", [(1, 33, 64), (127, 65, 96), (65, 17, 257), (300, 520, 1024), (257, 129, 4099)])
 def test_float_gemm(mode, shape, device):
+    """Float GEMMs with FP32 accumulation against a float64 product of the same operands.
+    Output gates: the reference's implementation rel-L2 (bf16 0.008, fp16 1e-3, fp32 1e-4,
+    engine.py gates) on the declared output dtype; FP32 output held to 1e-5 (FP32 accumulation
+    over K = 4099 alone is ~sqrt(K) * 2^-24 = 4e-6)."""
     m, n, k = shape
     rng = np.random.default_rng(5)
-    dt = torch.float16 if mode == "fp16" else torch.bfloat16
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[mode]
     a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(dt)
     b = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device).to(dt)
     expected = a.double().cpu().numpy() @ b.double().cpu().numpy().T
     y = gemm(a, b, mode, output_dtype=dt)
-    assert ref.metrics(y.float().cpu().numpy(), expected)["relative_l2"] < 0.008
+    gate = {"bf16": 0.008, "fp16": 1e-3, "fp32": 1e-4}[mode]
+    assert ref.metrics(y.float().cpu().numpy(), expected)["relative_l2"] < gate
     y32 = gemm(a, b, mode)
+    assert y32.dtype == torch.float32
     assert ref.metrics(np_of(y32), expected)["relative_l2"] < 1e-5
+
+
+def test_fp32_gemm_exact_small_integers(device):
+    """Small-integer FP32 operands make every product and partial sum exact, so the FP32 MFMA
+    result must equal the integer product exactly whatever its summation order."""
+    rng = np.random.default_rng(9)
+    a = rng.integers(-8, 9, (70, 300)).astype(np.float32)
+    b = rng.integers(-8, 9, (45, 300)).astype(np.float32)
+    y = gemm(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device), "fp32")
+    np.testing.assert_array_equal(np_of(y), (a.astype(np.int64) @ b.astype(np.int64).T).astype(np.float32))
 
 
 def test_repeat_runs_identical(device):
@@ -214,3 +230,23 @@ def test_repeat_runs_identical(device):
     first = gemm(*args, "int8", **kw)
     for _ in range(3):
         assert torch.equal(gemm(*args, "int8", **kw), first)
+
+
+@pytest.mark.parametrize("shape", [(64, 96, 128), (257, 130, 4096)])
+def test_mxint8_gemm(shape, device):
+    """MXINT8 linear against the float64 product of the dequantized operands (reference
+    dequantize, numerics.py:49-52): BF16 products are exact, so only FP32 accumulation order
+    differs (gate rel-L2 1e-5; the reference's own int8-quality gate is 0.05)."""
+    m, n, k = shape
+    rng = np.random.default_rng(13)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(device)
+    w = torch.from_numpy((rng.standard_normal((n, k)) * 0.02).astype(np.float32)).to(device)
+    aq, ae = quantize(a, "mxint8")
+    wq, we = quantize(w, "mxint8")
+    y = gemm(aq, wq, "mxint8", a_scales=ae, b_scales=we)
+    da = ref.dequantize(np_of(aq), np_of(ae), "mxint8").astype(np.float64)
+    dw = ref.dequantize(np_of(wq), np_of(we), "mxint8").astype(np.float64)
+    assert ref.metrics(np_of(y), da @ dw.T)["relative_l2"] < 1e-5
+    assert ref.metrics(np_of(y), a.double().cpu().numpy() @ w.double().cpu().numpy().T)["relative_l2"] < 0.05
+    yb = gemm(aq, wq, "mxint8", a_scales=ae, b_scales=we, output_dtype=torch.bfloat16)
+    assert yb.dtype == torch.bfloat16

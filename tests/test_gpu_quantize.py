@@ -168,3 +168,45 @@ def test_inputs_not_mutated_and_strided(device):
     rq, rs = ref.quantize_reference(view.float().cpu().numpy(), "int8")
     np.testing.assert_array_equal(np_of(q), rq)
     assert torch.equal(base, before)
+
+
+# ---- MXINT8 block quantizer (numerics.py:33-41) ----------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("shape", [(3, 32), (5, 4096), (129, 320), (2, 16384)])
+def test_mxint8_bit_exact(dtype, shape, device):
+    rng = np.random.default_rng(shape[0] * 7 + shape[1])
+    lo, hi = (-10, 10) if dtype == "fp16" else (-30, 30)  # stay inside the fp16 range
+    x = rng.standard_normal(shape).astype(np.float32) * np.exp2(rng.integers(lo, hi, (shape[0], 1)))
+    x[:, 64:96] = 0  # an all-zero block where present
+    xt = torch.from_numpy(x.astype(np.float32)).to(device).to(DTYPES[dtype])
+    q, e = quantize(xt, "mxint8")
+    assert q.dtype == torch.int8 and e.dtype == torch.uint8 and tuple(e.shape) == (shape[0], shape[1] // 32)
+    rq, re_ = ref.quantize_reference(xt.float().cpu().numpy(), "mxint8")
+    np.testing.assert_array_equal(np_of(e), re_)
+    np.testing.assert_array_equal(np_of(q), rq)
+
+
+def test_mxint8_kats_and_power_of_two_peaks(kats, device):
+    kat = kats["mx_scale_boundaries"]
+    q, e = quantize(torch.tensor(kat["x_rows"], dtype=torch.float32, device=device), "mxint8")
+    np.testing.assert_array_equal(np_of(q), np.array(kat["codes"], np.int8))
+    np.testing.assert_array_equal(np_of(e), np.array(kat["scales"], np.uint8))
+    # Block peaks within 40 ulps either side of 2^k for k in [-120, 120]: the rounded FP32 log2
+    # reaches k just below 2^k (exponent one higher than the peak's own), as in the reference.
+    peaks = []
+    for k in range(-120, 121, 3):
+        p = np.float32(2.0**k)
+        lo, hi = p, p
+        for _ in range(40):
+            lo, hi = np.nextafter(lo, np.float32(0)), np.nextafter(hi, np.float32(np.inf))
+            peaks += [lo, hi]
+    peaks = np.array(peaks, np.float32)
+    rng = np.random.default_rng(11)
+    x = (rng.uniform(-1, 1, (peaks.size, 32)) * peaks[:, None]).astype(np.float32)
+    x[:, 7] = peaks * np.where(rng.random(peaks.size) < 0.5, -1, 1).astype(np.float32)
+    q, e = quantize(torch.from_numpy(x).to(device), "mxint8")
+    rq, re_ = ref.quantize_reference(x, "mxint8")
+    np.testing.assert_array_equal(np_of(e), re_)
+    np.testing.assert_array_equal(np_of(q), rq)

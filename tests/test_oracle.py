@@ -371,3 +371,57 @@ def test_qk_rope_kats(kats):
     bad = ref.qk_rope_reference(rotated_first, gamma, np.empty((1, 0)), np.empty((1, 0)), projection_bf16=False,
                                 output_bf16=False)["output"]
     assert not np.allclose(good, bad)
+
+
+# ---- MXINT8 (numerics.py:33-41, 49-52) -----------------------------------------------------
+
+
+def test_mx_scale_boundaries_kat(kats):
+    kat = kats["mx_scale_boundaries"]  # tests/test_numerics.py:28-34
+    x = np.array(kat["x_rows"], dtype=np.float32)
+    q, s = ref.quantize_reference(x, "mxint8")
+    np.testing.assert_array_equal(q, np.array(kat["codes"], dtype=np.int8))
+    np.testing.assert_array_equal(s, np.array(kat["scales"], dtype=np.uint8))
+    np.testing.assert_array_equal(ref.dequantize(q, s, "mxint8"), x)
+
+
+def test_mx_zero_and_outlier_kat(kats):
+    kat = kats["mx_zero_and_outlier"]  # tests/test_numerics.py:17-25
+    x = np.zeros(kat["shape"], np.float32)
+    x[kat["outlier"]["row"], kat["outlier"]["col"]] = kat["outlier"]["value"]
+    q, s = ref.quantize_reference(x, "mxint8")
+    y = ref.dequantize(q, s, "mxint8")
+    assert np.all(y[0] == 0) and np.max(np.abs(y - x)) < 1
+    assert s.shape == (2, 2) and s.dtype == np.uint8
+
+
+def test_mx_exponent_matches_float32_log2_at_power_of_two_boundaries():
+    """The oracle takes log2 in float64 and rounds to float32 before the floor; the reference
+    floors numpy's float32 log2.  Peaks within 64 ulps either side of every power of two (where
+    the rounded log2 can reach the next integer) must give the same exponent."""
+    peaks = []
+    for k in range(-126, 128):
+        p = np.float32(2.0**k)
+        lo, hi = p, p
+        for _ in range(64):
+            lo = np.nextafter(lo, np.float32(0))
+            hi = np.nextafter(hi, np.float32(np.inf))
+            peaks += [lo, hi]
+        peaks.append(p)
+    peaks = np.array(peaks, dtype=np.float32)
+    peaks = peaks[np.isfinite(peaks) & (peaks > 0)]
+    literal = np.clip(np.floor(np.log2(np.maximum(peaks, np.finfo(np.float32).tiny))) - 6, -127, 127)
+    np.testing.assert_array_equal(ref.mx_exponent(peaks), literal.astype(np.float32))
+    # the rounded log2 really does reach the next power for some peaks below it
+    assert np.any(ref.mx_exponent(peaks) > np.frexp(peaks)[1] - 1 - 6)
+
+
+def test_mx_codes_bound_the_block_error():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((16, 256)) * np.exp2(rng.integers(-20, 20, (16, 1)))).astype(np.float32)
+    q, s = ref.quantize_reference(x, "mxint8")
+    step = np.repeat(np.exp2(s.astype(np.float64) - 127), 32, axis=1)
+    err = np.abs(ref.dequantize(q, s, "mxint8").astype(np.float64) - x)
+    clipped = np.abs(q) == 127  # a block peak in [127.5, 128) steps rounds past the clamp
+    assert np.all(err <= np.where(clipped, step, step / 2) * (1 + 1e-6))
+    assert np.all(np.abs(q.astype(np.int16)) <= 127)
