@@ -25,6 +25,7 @@
  *   unfused_norm             src/m5kernels/norm_hadamard.py:321-348
  *   projection_qk_rope       src/m5kernels/qk_rope.py:120-182
  *   qk_norm_rope             src/m5kernels/qk_rope.py:185-203
+ *   rms_quantize             src/m5kernels/rms_quant.py:41-117
  */
 #ifndef M5K_H
 #define M5K_H
@@ -214,6 +215,19 @@ int m5k_projection_qk_rope(const void* a, const void* b, int ab_dtype, int64_t m
  */
 int m5k_qk_norm_rope(const void* projected, int64_t m, int64_t n, const void* gamma, const void* cos,
                      const void* sin, int rope_half, float epsilon, void* y, void* stream);
+
+/*
+ * RMS dynamic INT8 quantization with the inverse RMS folded into the row scales.  Replaces
+ * rms_quant.rms_quantize (src/m5kernels/rms_quant.py:41-117, shaders/rms_quant.metal:1-97).
+ * x: [rows,k] F32/F16/BF16; gamma: FP32 [k]; signs: int8 +-1 [k]; block 1 (no transform, any
+ * k) or a power of two in [32,1024] dividing k.  ss = sum x^2, inv = 1/sqrt(ss/k + eps);
+ * v = fold ? (x*gamma)*s : ((x*inv)*gamma)*s; z = blockdiag(H_B) v; peak = max|z|;
+ * scales[row] = peak == 0 ? 1 : (peak * (fold ? inv : 1)) / 127;
+ * q = peak == 0 ? 0 : clamp(rint((z/peak)*127), -127, 127) int8 [rows,k].
+ */
+int m5k_rms_quantize(const void* x, int x_dtype, int64_t rows, int64_t k, const float* gamma,
+                     const int8_t* signs, int block, int fold_scale, float epsilon, int8_t* q,
+                     float* scales, void* stream);
 
 #ifdef __cplusplus
 }

@@ -8,6 +8,7 @@ behind a C ABI (include/m5k.h).  There is no CPU fallback.
 from .hip import gemm, gemm_i8_accumulators, quantize
 from .qk_rope import projection_qk_rope, qk_norm_rope
 from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
+from .rms_quant import rms_quantize
 from .norm_hadamard import (
     fused_gated_residual_norm_hadamard_quantize,
     fused_norm_hadamard_quantize,
@@ -28,4 +29,5 @@ __all__ = [
     "unfused_norm",
     "projection_qk_rope",
     "qk_norm_rope",
+    "rms_quantize",
 ]

@@ -535,3 +535,38 @@ def c_hadamard_f32(x, block, signs):
     y = np.empty_like(x)
     c_lib().oracle_hadamard_f32(_ptr(x), rows, k, int(block), _ptr(signs), _ptr(y))
     return y
+
+
+def rms_quantize_reference(x, gamma, signs=None, block_size=1, eps=1e-5):
+    """float64 RMS INT8 encoding with the inverse RMS folded into the row scales
+    (rms_quant_reference.py:24-89).
+
+    Z = (X * gamma) D H, r = 1 / sqrt(mean(X^2) + eps) over the original X; for a nonzero row
+    Q = clip(rint(Z / (max|Z| / 127)), -127, 127) and S = max|Z| / 127 * r; a zero row of Z gives
+    Q = 0 and S = 1.  Returns a dict with the same keys as the reference."""
+    if isinstance(eps, bool) or not isinstance(eps, (int, float, np.floating)) or not np.isfinite(eps) or eps <= 0:
+        raise ValueError("eps must be a positive finite real scalar")
+    x = np.asarray(x, dtype=np.float64)
+    gamma = np.asarray(gamma, dtype=np.float64)
+    if x.ndim != 2 or not all(x.shape):
+        raise ValueError("input must have nonempty shape [M,K]")
+    if gamma.shape != (x.shape[1],):
+        raise ValueError("gamma must have shape [K]")
+    if not (np.isfinite(x).all() and np.isfinite(gamma).all()):
+        raise ValueError("input and gamma must be finite")
+    inverse_rms = 1.0 / np.sqrt(np.mean(x * x, axis=1) + float(eps))
+    unscaled = block_hadamard_reference(x * gamma, block_size, signs)
+    peak = np.max(np.abs(unscaled), axis=1)
+    nonzero = peak != 0
+    unscaled_scales = np.where(nonzero, peak / 127.0, 1.0)
+    scales = np.where(nonzero, unscaled_scales * inverse_rms, 1.0)
+    quantized = np.clip(np.rint(unscaled / unscaled_scales[:, None]), -127, 127).astype(np.int8)
+    return {
+        "normalized_rotated": unscaled * inverse_rms[:, None],
+        "quantized": quantized,
+        "scales": scales,
+        "dequantized": quantized.astype(np.float64) * scales[:, None],
+        "unscaled_rotated": unscaled,
+        "inverse_rms": inverse_rms,
+        "unscaled_scales": unscaled_scales,
+    }

@@ -122,3 +122,32 @@ def test_rotate_implementation_switch():
         rotate(x, 256, signs, implementation="mlx")
     with pytest.raises(ValueError, match="unknown Hadamard implementation"):
         rotate(x, 256, signs, implementation="cuda")
+
+
+def test_rms_quantize_validation():
+    """rms_quant.py:56-100: metadata errors, checked before any device work."""
+    from m5kernels_amd import rms_quantize
+
+    x, g, s = torch.zeros(2, 64), torch.ones(64), torch.ones(64, dtype=torch.int8)
+    with pytest.raises(ValueError, match="shape"):
+        rms_quantize(torch.zeros(64), g, s)
+    with pytest.raises(ValueError, match="gamma"):
+        rms_quantize(x, torch.ones(64, dtype=torch.float16), s)
+    with pytest.raises(ValueError, match="signs"):
+        rms_quantize(x, g, torch.ones(64))
+    with pytest.raises(ValueError, match="power of two"):
+        rms_quantize(x, g, s, 3)
+    with pytest.raises(NotImplementedError, match="supported blocks"):
+        rms_quantize(x, g, s, 16)
+    with pytest.raises(NotImplementedError, match="divisible"):
+        rms_quantize(torch.zeros(2, 96), torch.ones(96), torch.ones(96, dtype=torch.int8), 64)
+    with pytest.raises(NotImplementedError, match="threadgroup"):
+        rms_quantize(x, g, s, threads=64)
+    with pytest.raises(ValueError, match="boolean"):
+        rms_quantize(x, g, s, fold_scale=1)
+    with pytest.raises(ValueError, match="epsilon"):
+        rms_quantize(x, g, s, epsilon=0)
+    with pytest.raises(ValueError, match="identifier"):
+        rms_quantize(x, g, s, tag="1bad")
+    with pytest.raises(ValueError, match="ROCm device"):
+        rms_quantize(x, g, s)

@@ -425,3 +425,60 @@ def test_mx_codes_bound_the_block_error():
     clipped = np.abs(q) == 127  # a block peak in [127.5, 128) steps rounds past the clamp
     assert np.all(err <= np.where(clipped, step, step / 2) * (1 + 1e-6))
     assert np.all(np.abs(q.astype(np.int16)) <= 127)
+
+
+# ---- RMS scale-folded quantizer (rms_quant_reference.py:24-89) --------------------------------
+
+
+def _dense_h(block):
+    return np.array([[(-1) ** bin(i & j).count("1") for j in range(block)] for i in range(block)], np.float64) / math.sqrt(block)
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 128])
+@pytest.mark.parametrize("signed", [False, True])
+def test_rms_quantize_matches_materialized_dense_definition(block_size, signed):
+    """tests/test_rms_quant_reference.py:17-67: normalize with fsum statistics, multiply gamma,
+    apply the dense Kronecker H; codes equal, scales to 3e-14."""
+    rng = np.random.default_rng(59)
+    width = 3 * block_size
+    x = rng.normal(size=(5, width))
+    gamma = rng.normal(size=width)
+    gamma[0] = 0
+    x[0, 0] *= 1000
+    signs = ref.hadamard_signs(width, 61) if signed else None
+    inv = np.array([1.0 / math.sqrt(math.fsum(float(v) ** 2 for v in row) / width + 1e-5) for row in x])
+    normalized = x * inv[:, None] * gamma
+    expected = (normalized * (signs if signed else 1)) @ np.kron(np.eye(3), _dense_h(block_size))
+    peak = np.max(np.abs(expected), axis=1)
+    exp_s = np.where(peak == 0, 1.0, peak / 127)
+    exp_q = np.clip(np.rint(expected / exp_s[:, None]), -127, 127).astype(np.int8)
+    got = ref.rms_quantize_reference(x, gamma, signs, block_size)
+    np.testing.assert_allclose(got["inverse_rms"], inv, rtol=3e-14)
+    np.testing.assert_allclose(got["scales"], exp_s, rtol=3e-14)
+    np.testing.assert_array_equal(got["quantized"], exp_q)
+
+
+def test_rms_statistics_use_original_input_kat():
+    """tests/test_rms_quant_reference.py:91-101."""
+    x = np.array([[1.0, 2.0, -4.0, 8.0]])
+    gamma = np.array([-100.0, 0.0, 2.0, 0.01])
+    got = ref.rms_quantize_reference(x, gamma, block_size=2)
+    inv = 1 / math.sqrt((1 + 4 + 16 + 64) / 4 + 1e-5)
+    np.testing.assert_allclose(got["inverse_rms"], [inv], rtol=0, atol=0)
+    peak = np.max(np.abs((x * gamma) @ np.kron(np.eye(2), _dense_h(2))))
+    np.testing.assert_allclose(got["scales"], [peak / 127 * inv], rtol=3e-15)
+
+
+def test_rms_ties_zero_rows_and_epsilon():
+    """tests/test_rms_quant_reference.py:104-123 and :70-88."""
+    got = ref.rms_quantize_reference(np.array([[127.0, 2.5, 3.5, -2.5, -3.5, 0.0, -127.0, 1.5]]), np.ones(8))
+    np.testing.assert_array_equal(got["quantized"], [[127, 2, 4, -2, -4, 0, -127, 2]])
+    np.testing.assert_array_equal(got["scales"], got["inverse_rms"])
+    zero = ref.rms_quantize_reference(np.ones((3, 8)), np.zeros(8), block_size=4)
+    np.testing.assert_array_equal(zero["quantized"], 0)
+    np.testing.assert_array_equal(zero["scales"], np.ones(3))
+    rng = np.random.default_rng(67)
+    x, g = rng.normal(size=(3, 24)) * 0.01, rng.normal(size=24)
+    small, large = ref.rms_quantize_reference(x, g, block_size=8, eps=1e-8), ref.rms_quantize_reference(x, g, block_size=8, eps=1.0)
+    np.testing.assert_array_equal(small["quantized"], large["quantized"])
+    assert np.all(small["scales"] > large["scales"])
