@@ -247,6 +247,25 @@ def _qk_case(torch, dev, m=9914, k=4096, n=4096):
     }
 
 
+def _rms_case(torch, dev, m=4096, k=4096, block=256):
+    """RMS scale-folded INT8 quantizer (rms_quantize) on a bf16 [m, k] activation, H256."""
+    from m5kernels_amd import rms_quantize
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    x = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn((k,), generator=g, device=dev)).float()
+    signs = torch.ones(k, dtype=torch.int8, device=dev)
+    nbytes = 3 * m * k + 4 * m + 5 * k
+    out = {"m": m, "k": k, "block": block}
+    for fold in (True, False):
+        t = time_op(torch, lambda: rms_quantize(x, gamma, signs, block, fold_scale=fold))
+        key = "fold" if fold else "no_fold"
+        out[f"{key}_ms"] = t["avg_ms"]
+        out[f"{key}_GBps"] = nbytes / (t["avg_ms"] * 1e-3) / 1e9
+        out[f"{key}_frac_of_hbm_peak"] = out[f"{key}_GBps"] / PEAK_HBM_GBS
+    return out
+
+
 def extras(torch, dev):
     """Every other configuration: parity-test shapes timed on the same GPU (not the headline)."""
     out = {}
@@ -258,6 +277,7 @@ def extras(torch, dev):
         ("fused_prep_m4096", lambda: _prep_case(torch, dev, 4096)),
         ("fused_prep_m9914", lambda: _prep_case(torch, dev, 9914)),
         ("qk_rope_m9914", lambda: _qk_case(torch, dev)),
+        ("rms_quantize_m4096_h256", lambda: _rms_case(torch, dev)),
     ]
     for name, fn in cases:
         log(f"[bench] extra {name}")

@@ -26,6 +26,7 @@ struct EpiParams {
   const uint16_t* residual;
   const uint16_t* gate;
   const int32_t* gate_map;
+  int coalesced;  // 16-bit output with N % 8 == 0 and 16-byte aligned c / residual / gate
 };
 
 // RAW: write INT32 accumulators (I8 only).
@@ -44,6 +45,56 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint
   AccTile<MODE, G> acc;
   if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+
+  auto scaled = [&](int m, int n, auto v) {
+    float value;
+    if constexpr (MODE == I8 || MODE == F8) value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
+    else value = v;
+    if constexpr (BIAS != EPI_NONE) {
+      const int64_t boff = BIAS == EPI_TABLE ? (int64_t)p.bias_map[m] * N : 0;
+      value = value + p.bias[boff + n];
+    }
+    return value;
+  };
+
+  // 16-bit outputs: stage the rounded tile (the BF16 branch for the gated form) in the LDS the
+  // main loop has released, then write whole 512-byte tile rows with 16-byte stores.
+  if constexpr (!RAW && (OUT_DT == M5K_BF16 || OUT_DT == M5K_F16)) {
+    if (p.coalesced) {
+      uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
+      for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
+        const float value = (m < M && n < N) ? scaled(m, n, v) : 0.0f;
+        tile[(m - m0) * BN + (n - n0)] = static_cast<uint16_t>(
+            GATE != EPI_NONE || OUT_DT == M5K_BF16 ? f32_to_bf16_bits(value) : f32_to_f16_bits(value));
+      });
+      __syncthreads();
+      for (int c = threadIdx.x; c < BM * BN / 8; c += G::THREADS) {
+        const int r = c >> 5, cc = c & 31;
+        const int m = m0 + r, n = n0 + 8 * cc;
+        if (m >= M || n >= N) continue;  // N % 8 == 0: a chunk is wholly in or out
+        uint4 w = *reinterpret_cast<const uint4*>(tile + r * BN + 8 * cc);
+        const int64_t idx = (int64_t)m * N + n;
+        if constexpr (GATE != EPI_NONE) {
+          const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;
+          const uint4 rw = *reinterpret_cast<const uint4*>(p.residual + idx);
+          const uint4 gw = *reinterpret_cast<const uint4*>(p.gate + goff + n);
+          const uint32_t bs[4] = {w.x, w.y, w.z, w.w}, rs[4] = {rw.x, rw.y, rw.z, rw.w},
+                         gs[4] = {gw.x, gw.y, gw.z, gw.w};
+          uint32_t out[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float lo = bf16_bits_to_f32(rs[t] & 0xFFFFu) +
+                             bf16_bits_to_f32(bs[t] & 0xFFFFu) * bf16_bits_to_f32(gs[t] & 0xFFFFu);
+            const float hi = bf16_bits_to_f32(rs[t] >> 16) + bf16_bits_to_f32(bs[t] >> 16) * bf16_bits_to_f32(gs[t] >> 16);
+            out[t] = f32x2_to_bf16x2(lo, hi);
+          }
+          w = make_uint4(out[0], out[1], out[2], out[3]);
+        }
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + idx) = w;
+      }
+      return;
+    }
+  }
 
   for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
     if (m >= M || n >= N) return;
@@ -83,10 +134,12 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   const dim3 grid(static_cast<unsigned>(tiles)), block(KernelGrid::THREADS);
   auto* A = static_cast<const uint8_t*>(a);
   auto* B = static_cast<const uint8_t*>(b);
+  EpiParams q = p;
+  q.coalesced = n % 8 == 0 && aligned16(p.c) && (p.residual == nullptr || (aligned16(p.residual) && aligned16(p.gate)));
   if (aligned)
-    gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, p);
+    gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
   else
-    gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, p);
+    gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
   return launch_status(name);
 }
 
