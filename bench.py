@@ -80,11 +80,16 @@ def cpu_baseline(torch, a, wq, ws, y, target_s):
 
 
 def time_op(torch, fn, reps=20, warm=3):
-    """Device time of fn: HIP events on the current stream around each of `reps` launches."""
+    """Device time of fn: HIP events on the current stream around each of `reps` launches.
+
+    A GPU spin is queued first so the host enqueues every launch before the first one runs:
+    the launches then execute back to back and the events measure device time only, not the
+    Python wrapper's per-call overhead (which exceeds the run time of the smaller kernels)."""
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda._sleep(50_000_000)
     for e0, e1 in evs:
         e0.record()
         fn()
