@@ -252,6 +252,32 @@ def _qk_case(torch, dev, m=9914, k=4096, n=4096):
     }
 
 
+def _qkv_case(torch, dev, m=4096, heads=32, k=4096):
+    """Grouped Q/K/V projection (weights [heads, 3, 128, K]) with per-head RMSNorm + RoPE on Q/K
+    and V passthrough, INT8 online (quantize + one fused kernel), R = 64, base 10000."""
+    from m5kernels_amd import projection_qkv_rope, quantize
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    bf = torch.bfloat16
+    x = torch.randn((m, k), generator=g, device=dev).to(bf)
+    w = (torch.randn((heads * 384, k), generator=g, device=dev) * 0.02).to(bf)
+    qg = (1 + 0.02 * torch.randn((128,), generator=g, device=dev)).to(bf)
+    kg = (1 + 0.02 * torch.randn((128,), generator=g, device=dev)).to(bf)
+    theta = 10000.0 ** (-torch.arange(64, device=dev, dtype=torch.float64) * 2 / 128)
+    ang = torch.arange(m, device=dev, dtype=torch.float64)[:, None] * theta[None, :]
+    cos, sin = ang.cos().float().to(bf), ang.sin().float().to(bf)
+    wq, ws = quantize(w, "int8")
+    ops = 2.0 * m * heads * 384 * k
+
+    def online():
+        q, s = quantize(x, "int8")
+        return projection_qkv_rope(q, wq, qg, kg, cos, sin, "int8", a_scales=s, w_scales=ws)
+
+    t = time_op(torch, online)
+    return {"m": m, "heads": heads, "k": k, "int8_online_ms": t["avg_ms"],
+            "int8_online_TOPS": ops / (t["avg_ms"] * 1e-3) / 1e12}
+
+
 def _rms_case(torch, dev, m=4096, k=4096, block=256):
     """RMS scale-folded INT8 quantizer (rms_quantize) on a bf16 [m, k] activation, H256."""
     from m5kernels_amd import rms_quantize
@@ -283,6 +309,7 @@ def extras(torch, dev):
         ("fused_prep_m9914", lambda: _prep_case(torch, dev, 9914)),
         ("qk_rope_m9914", lambda: _qk_case(torch, dev)),
         ("rms_quantize_m4096_h256", lambda: _rms_case(torch, dev)),
+        ("grouped_qkv_m4096_h32", lambda: _qkv_case(torch, dev)),
     ]
     for name, fn in cases:
         log(f"[bench] extra {name}")

@@ -217,6 +217,21 @@ int m5k_qk_norm_rope(const void* projected, int64_t m, int64_t n, const void* ga
                      const void* sin, int rope_half, float epsilon, void* y, void* stream);
 
 /*
+ * Grouped Q/K/V projection in the H3 runtime's native layout
+ * (integrations/h3/qkv_candidate.metal:5-81, reference math qkv_reference.h:15-35).
+ * b: [heads*3*128, k] weight rows ordered [head][stream Q,K,V][channel]; a: [m,k] (INT8
+ * with a_scales/b_scales, or BF16).  Every 128-column block is rounded to BF16 as in
+ * m5k_projection_qk_rope; Q blocks then take q_gamma and K blocks k_gamma through the same
+ * per-head RMSNorm + split-half RoPE (cos/sin [m, rope_half]); V blocks are the rounded
+ * projection.  q_out, k_out, v_out: BF16 [heads, m, 128], 16-byte aligned.
+ */
+int m5k_projection_qkv_rope(const void* a, const void* b, int ab_dtype, int64_t m, int64_t heads,
+                            int64_t k, const float* a_scales, const float* b_scales,
+                            const void* q_gamma, const void* k_gamma, const void* cos,
+                            const void* sin, int rope_half, float epsilon, void* q_out,
+                            void* k_out, void* v_out, void* stream);
+
+/*
  * RMS dynamic INT8 quantization with the inverse RMS folded into the row scales.  Replaces
  * rms_quant.rms_quantize (src/m5kernels/rms_quant.py:41-117, shaders/rms_quant.metal:1-97).
  * x: [rows,k] F32/F16/BF16; gamma: FP32 [k]; signs: int8 +-1 [k]; block 1 (no transform, any

@@ -29,13 +29,34 @@ using m5k::gemm::detail::KernelGrid;
 constexpr int HEAD = 128;
 
 struct QkParams {
-  const uint16_t* gamma;  // bf16 [128]
+  const uint16_t* gamma;  // bf16 [128] (Q gamma in the grouped layout)
   const uint16_t* cos;    // bf16 [M, R]
   const uint16_t* sin;    // bf16 [M, R]
   int rope_half;          // R in [0, 64]
   float eps;
-  uint16_t* y;            // bf16 [N/128, M, 128]
+  uint16_t* y;            // bf16 [N/128, M, 128] (Q output in the grouped layout)
+  // Grouped Q/K/V layout: weight rows [heads, 3, 128]; 128-column block c is head c / 3,
+  // stream c % 3 (0 = Q, 1 = K, 2 = V).  V is the BF16 projection itself.
+  int grouped;
+  const uint16_t* k_gamma;  // bf16 [128]
+  uint16_t* k_out;          // bf16 [heads, M, 128]
+  uint16_t* v_out;          // bf16 [heads, M, 128]
 };
+
+// Destination of 128-column block `block`: head index, output tensor and gamma (nullptr for V).
+struct BlockDst {
+  int head;
+  uint16_t* out;
+  const uint16_t* gamma;
+};
+
+__device__ __forceinline__ BlockDst block_dst(const QkParams& p, int block) {
+  if (!p.grouped) return BlockDst{block, p.y, p.gamma};
+  const int head = block / 3, stream = block - 3 * head;
+  return stream == 0 ? BlockDst{head, p.y, p.gamma}
+         : stream == 1 ? BlockDst{head, p.k_out, p.k_gamma}
+                       : BlockDst{head, p.v_out, nullptr};
+}
 
 // Normalize + rotate one (row, head).  lg in [0,16) owns channels [8 lg, 8 lg + 8); z holds
 // them; partner(d) returns channel d of the same (row, head).  All 16 lanes of the group must
@@ -87,9 +108,9 @@ struct LaneRope {
   bool rot, lower;
 };
 
-__device__ __forceinline__ LaneRope lane_rope(const QkParams& p, int lg) {
+__device__ __forceinline__ LaneRope lane_rope(const QkParams& p, const uint16_t* gamma, int lg) {
   LaneRope r;
-  const uint4 g = *reinterpret_cast<const uint4*>(p.gamma + 8 * lg);
+  const uint4 g = *reinterpret_cast<const uint4*>(gamma + 8 * lg);
   const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -178,10 +199,11 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   const int heads_here = (N - n0) >= BN ? 2 : 1;  // N is a multiple of 128
 
   // Fast path: issue the per-row cos/sin loads of this group's rows before staging the tile.
-  LaneRope lr;
+  LaneRope lr, lrk;  // Q (or single-projection) gamma; K gamma in the grouped layout
   uint4 cw[ROWS_PER_GROUP], sw[ROWS_PER_GROUP];
   if (fast) {
-    lr = lane_rope(p, lg);
+    lr = lane_rope(p, p.gamma, lg);
+    if (p.grouped) lrk = lane_rope(p, p.k_gamma, lg);
 #pragma unroll
     for (int i = 0; i < ROWS_PER_GROUP; ++i) {
       const int row = m0 + group + GROUPS * i;
@@ -210,11 +232,16 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
       for (int h = 0; h < 2; ++h) {
         if (h >= heads_here) continue;
         const uint16_t* src = tile + local_row * BN + h * HEAD;
+        const BlockDst d = block_dst(p, n0 / HEAD + h);  // uniform across the group
+        const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
+        uint4* dst = reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg);
+        if (d.gamma == nullptr) {  // V: the rounded projection
+          *dst = w;
+          continue;
+        }
         float z[8];
-        unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
-        const uint4 out = norm_rope_fast(z, lr, cw[i], sw[i], p.eps);
-        const int head = n0 / HEAD + h;
-        *reinterpret_cast<uint4*>(p.y + (static_cast<int64_t>(head) * M + row) * HEAD + 8 * lg) = out;
+        unpack8_bf16(w, z);
+        *dst = norm_rope_fast(z, d.gamma == p.gamma ? lr : lrk, cw[i], sw[i], p.eps);
       }
     }
     return;
@@ -222,12 +249,21 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   for (int q = group; q < BM * 2; q += GROUPS) {
     const int local_row = q >> 1, local_head = q & 1;
     const int row = m0 + local_row;
-    const int head = n0 / HEAD + local_head;
-    if (row >= M || head * HEAD >= N) continue;  // uniform across the 16-lane group
+    const int block = n0 / HEAD + local_head;
+    if (row >= M || block * HEAD >= N) continue;  // uniform across the 16-lane group
     const uint16_t* src = tile + local_row * BN + local_head * HEAD;
+    const BlockDst d = block_dst(p, block);
+    if (d.gamma == nullptr) {
+      *reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg) =
+          *reinterpret_cast<const uint4*>(src + 8 * lg);
+      continue;
+    }
+    QkParams ps = p;
+    ps.gamma = d.gamma;
+    ps.y = d.out;
     float z[8];
     unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
-    norm_rope_16(z, [&](int d) { return bf16_bits_to_f32(src[d]); }, p, row, M, head, lg);
+    norm_rope_16(z, [&](int dd) { return bf16_bits_to_f32(src[dd]); }, ps, row, M, d.head, lg);
   }
 }
 
@@ -245,7 +281,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
   float z[8];
   unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
   if (fast) {
-    const LaneRope lr = lane_rope(p, lg);
+    const LaneRope lr = lane_rope(p, p.gamma, lg);
     uint4 cw, sw;
     lane_cos_sin(p, lr, row, lg, cw, sw);
     const uint4 out = norm_rope_fast(z, lr, cw, sw, p.eps);
@@ -257,7 +293,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
 
 // The fast path needs whole 8-channel lanes per RoPE half and 16-byte aligned tables.
 inline int fast_rope(const QkParams& p) {
-  return p.rope_half % 8 == 0 && aligned16(p.gamma) && (p.rope_half == 0 || (aligned16(p.cos) && aligned16(p.sin)));
+  return p.rope_half % 8 == 0 && aligned16(p.gamma) && (!p.grouped || aligned16(p.k_gamma)) &&
+         (p.rope_half == 0 || (aligned16(p.cos) && aligned16(p.sin)));
 }
 
 template <int MODE>
@@ -303,7 +340,7 @@ extern "C" int m5k_projection_qk_rope(const void* a, const void* b, int ab_dtype
   if (int rc = check_norm_args(m, n, gamma, cos, sin, rope_half, epsilon, y, name)) return rc;
   M5K_REQUIRE(a && b && k > 0, "%s: null operand or empty K", name);
   QkParams p{static_cast<const uint16_t*>(gamma), static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
-             rope_half, epsilon, static_cast<uint16_t*>(y)};
+             rope_half, epsilon, static_cast<uint16_t*>(y), 0, nullptr, nullptr, nullptr};
   hipStream_t st = as_stream(stream);
   if (ab_dtype == M5K_I8) {
     M5K_REQUIRE(a_scales && b_scales, "%s: INT8 needs a_scales and b_scales", name);
@@ -321,11 +358,37 @@ extern "C" int m5k_qk_norm_rope(const void* projected, int64_t m, int64_t n, con
   if (int rc = check_norm_args(m, n, gamma, cos, sin, rope_half, epsilon, y, name)) return rc;
   M5K_REQUIRE(projected && aligned16(projected), "%s: projection must be a 16-byte aligned pointer", name);
   QkParams p{static_cast<const uint16_t*>(gamma), static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
-             rope_half, epsilon, static_cast<uint16_t*>(y)};
+             rope_half, epsilon, static_cast<uint16_t*>(y), 0, nullptr, nullptr, nullptr};
   const int64_t groups = m * (n / HEAD);
   const int64_t blocks = (groups + 15) / 16;
   M5K_REQUIRE(blocks <= 0x7FFFFFFF, "%s: input too large", name);
   qk_norm_rope_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(projected), m, n, p, fast_rope(p));
   return launch_status(name);
+}
+
+extern "C" int m5k_projection_qkv_rope(const void* a, const void* b, int ab_dtype, int64_t m, int64_t heads, int64_t k,
+                                       const float* a_scales, const float* b_scales, const void* q_gamma,
+                                       const void* k_gamma, const void* cos, const void* sin, int rope_half,
+                                       float epsilon, void* q_out, void* k_out, void* v_out, void* stream) {
+  clear_error();
+  const char* name = "m5k_projection_qkv_rope";
+  M5K_REQUIRE(heads > 0 && heads * 3 * HEAD <= 0x7FFFFFFF, "%s: bad head count %lld", name, (long long)heads);
+  const int64_t n = heads * 3 * HEAD;
+  if (int rc = check_norm_args(m, n, q_gamma, cos, sin, rope_half, epsilon, q_out, name)) return rc;
+  M5K_REQUIRE(a && b && k > 0 && k_gamma && k_out && v_out, "%s: null pointer or empty K", name);
+  M5K_REQUIRE(aligned16(k_out) && aligned16(v_out), "%s: outputs must be 16-byte aligned", name);
+  QkParams p{static_cast<const uint16_t*>(q_gamma), static_cast<const uint16_t*>(cos),
+             static_cast<const uint16_t*>(sin),     rope_half,
+             epsilon,                               static_cast<uint16_t*>(q_out),
+             1,                                     static_cast<const uint16_t*>(k_gamma),
+             static_cast<uint16_t*>(k_out),         static_cast<uint16_t*>(v_out)};
+  hipStream_t st = as_stream(stream);
+  if (ab_dtype == M5K_I8) {
+    M5K_REQUIRE(a_scales && b_scales, "%s: INT8 needs a_scales and b_scales", name);
+    M5K_REQUIRE(k <= 131071, "%s: K exceeds the INT32 worst-case bound 131071", name);
+    return launch_fused<I8>(a, b, m, n, k, a_scales, b_scales, p, st);
+  }
+  M5K_REQUIRE(ab_dtype == M5K_BF16, "%s: operands must be INT8 or BF16", name);
+  return launch_fused<BF16>(a, b, m, n, k, nullptr, nullptr, p, st);
 }

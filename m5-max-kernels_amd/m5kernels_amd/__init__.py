@@ -6,7 +6,7 @@ behind a C ABI (include/m5k.h).  There is no CPU fallback.
 """
 
 from .hip import gemm, gemm_i8_accumulators, quantize
-from .qk_rope import projection_qk_rope, qk_norm_rope
+from .qk_rope import projection_qk_rope, projection_qkv_rope, qk_norm_rope
 from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
 from .rms_quant import rms_quantize
 from .norm_hadamard import (
@@ -29,5 +29,6 @@ __all__ = [
     "unfused_norm",
     "projection_qk_rope",
     "qk_norm_rope",
+    "projection_qkv_rope",
     "rms_quantize",
 ]

@@ -140,3 +140,52 @@ def qk_norm_rope(projected, gamma, cos, sin, *, epsilon=1e-5, threads=128):
         _lib.ptr(y), _lib.stream_of(projected),
     )
     return y
+
+
+def projection_qkv_rope(a, w, q_gamma, k_gamma, cos, sin, mode="int8", *, a_scales=None, w_scales=None,
+                        epsilon=1e-6):
+    """Grouped Q/K/V projection in the H3 runtime's native layout (integrations/h3/
+    qkv_candidate.metal, qkv_reference.h:15-35): W rows [heads, 3, 128] ordered Q, K, V per head.
+
+    Returns BF16 (Q, K, V), each [heads, M, 128].  Q and K get the per-head RMSNorm (q_gamma /
+    k_gamma) and split-half RoPE of projection_qk_rope; V is the BF16-rounded projection."""
+    if mode not in ("int8", "bf16"):
+        raise NotImplementedError("grouped Q/K/V projection supports INT8 or BF16 only")
+    if a.dim() != 2 or w.dim() != 2 or not all(a.shape) or not all(w.shape):
+        raise ValueError("A and W must be nonempty matrices")
+    m, k = a.shape
+    n, kw = w.shape
+    if k != kw:
+        raise ValueError("K mismatch")
+    if n % (3 * HEAD_DIM):
+        raise ValueError("W must have heads*3*128 rows ordered [head][Q,K,V][channel]")
+    heads = n // (3 * HEAD_DIM)
+    expected = torch.int8 if mode == "int8" else torch.bfloat16
+    if a.dtype != expected or w.dtype != expected:
+        raise ValueError(f"A and W must both have {mode} dtype")
+    if mode == "int8":
+        if k > 131071:
+            raise NotImplementedError("INT32 worst-case overflow bound exceeded for signed INT8")
+        if (a_scales is None or w_scales is None or tuple(a_scales.shape) != (m,) or tuple(w_scales.shape) != (n,)
+                or a_scales.dtype != torch.float32 or w_scales.dtype != torch.float32):
+            raise ValueError("INT8 requires float32 a_scales[M] and w_scales[heads*384]")
+    elif a_scales is not None or w_scales is not None:
+        raise ValueError("BF16 projection does not accept quantization scales")
+    rope_half, epsilon = _validate_norm(m, n, q_gamma, cos, sin, epsilon)
+    if tuple(k_gamma.shape) != (HEAD_DIM,) or k_gamma.dtype != torch.bfloat16:
+        raise ValueError("k_gamma must be a shared bfloat16 vector of length 128")
+    a = _lib.device_tensor(a, "a")
+    w = _lib.device_tensor(w, "w")
+    q_gamma, cos, sin = _tables(q_gamma, cos, sin)
+    k_gamma = _lib.aligned_device_tensor(k_gamma, "k_gamma")
+    q, kk, v = (torch.empty((heads, m, HEAD_DIM), dtype=torch.bfloat16, device=a.device) for _ in range(3))
+    if mode == "int8":
+        a_scales = _lib.device_tensor(a_scales, "a_scales")
+        w_scales = _lib.device_tensor(w_scales, "w_scales")
+    _lib.call(
+        "m5k_projection_qkv_rope",
+        _lib.ptr(a), _lib.ptr(w), _lib.dtype_code(a), m, heads, k, _lib.ptr(a_scales), _lib.ptr(w_scales),
+        _lib.ptr(q_gamma), _lib.ptr(k_gamma), _lib.ptr(cos), _lib.ptr(sin), int(rope_half), float(epsilon),
+        _lib.ptr(q), _lib.ptr(kk), _lib.ptr(v), _lib.stream_of(a),
+    )
+    return q, kk, v

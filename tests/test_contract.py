@@ -151,3 +151,20 @@ def test_rms_quantize_validation():
         rms_quantize(x, g, s, tag="1bad")
     with pytest.raises(ValueError, match="ROCm device"):
         rms_quantize(x, g, s)
+
+
+def test_grouped_qkv_validation():
+    from m5kernels_amd import projection_qkv_rope
+
+    g = torch.ones(128, dtype=torch.bfloat16)
+    cs = torch.ones(4, 48, dtype=torch.bfloat16)
+    a = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="heads\\*3\\*128"):
+        projection_qkv_rope(a, torch.zeros(256, 64, dtype=torch.bfloat16), g, g, cs, cs, "bf16")
+    with pytest.raises(NotImplementedError):
+        projection_qkv_rope(a, torch.zeros(384, 64, dtype=torch.bfloat16), g, g, cs, cs, "fp8")
+    with pytest.raises(ValueError, match="k_gamma"):
+        projection_qkv_rope(a, torch.zeros(384, 64, dtype=torch.bfloat16), g, torch.ones(64, dtype=torch.bfloat16),
+                            cs, cs, "bf16")
+    with pytest.raises(ValueError, match="ROCm device"):
+        projection_qkv_rope(a, torch.zeros(384, 64, dtype=torch.bfloat16), g, g, cs, cs, "bf16")

@@ -214,3 +214,37 @@ def test_qk_configuration_shape(device):
                                          _f32(sin)[rows], epsilon=1e-6)["output"]
         _check(y[:, rows], expected)
         assert math.isfinite(float(y.float().abs().max()))
+
+
+# ---- grouped Q/K/V layout (integrations/h3/qkv_candidate.metal, qkv_reference.h) ------------
+
+
+@pytest.mark.parametrize("mode", ["int8", "bf16"])
+@pytest.mark.parametrize("rope_half", [48, 5])
+@pytest.mark.parametrize("m,heads", [(300, 3), (129, 2)])
+def test_grouped_qkv_equals_staged(mode, rope_half, m, heads, device):
+    """Q and K of the grouped layout equal the staged qk_norm_rope of their projection blocks
+    bit for bit; V equals the BF16 projection itself, head-major.  Three heads give 1152
+    columns, so 256-column tiles mix streams and heads; M = 300 / 129 leaves partial row tiles."""
+    from m5kernels_amd import projection_qkv_rope
+
+    rng = np.random.default_rng(31 + m + heads + rope_half)
+    k = 512
+    x = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(torch.bfloat16)
+    w = torch.from_numpy((rng.standard_normal((heads * 384, k)) * 0.05).astype(np.float32)).to(device).to(torch.bfloat16)
+    q_gamma, cos, sin = _tables(rng, m, device, rope_half)
+    k_gamma = torch.from_numpy(rng.uniform(0.5, 1.5, 128).astype(np.float32)).to(device).to(torch.bfloat16)
+    if mode == "int8":
+        a, sa = quantize(x, "int8")
+        b, sb = quantize(w, "int8")
+        q, kk, v = projection_qkv_rope(a, b, q_gamma, k_gamma, cos, sin, "int8", a_scales=sa, w_scales=sb)
+        proj = gemm(a, b, "int8", a_scales=sa, b_scales=sb, output_dtype=torch.bfloat16)
+    else:
+        q, kk, v = projection_qkv_rope(x, w, q_gamma, k_gamma, cos, sin, "bf16")
+        proj = gemm(x, w, "bf16", output_dtype=torch.bfloat16)
+    blocks = proj.view(m, heads, 3, 128)
+    for stream, (out, gamma) in enumerate(((q, q_gamma), (kk, k_gamma))):
+        staged = qk_norm_rope(blocks[:, :, stream, :].reshape(m, heads * 128), gamma, cos, sin, epsilon=1e-6)
+        assert torch.equal(out, staged), f"stream {stream}"
+    assert torch.equal(v, blocks[:, :, 2, :].permute(1, 0, 2).contiguous())
+    assert q.shape == kk.shape == v.shape == (heads, m, 128)
