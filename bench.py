@@ -278,6 +278,35 @@ def _qkv_case(torch, dev, m=4096, heads=32, k=4096):
             "int8_online_TOPS": ops / (t["avg_ms"] * 1e-3) / 1e12}
 
 
+def _chain_case(torch, dev, m=4096, h=5376, pk=7168, n=14336):
+    """Gate-placement chain (gate_epilogue_chain.py:95-150): resident INT8 previous activation ->
+    W8A8 projection [pk -> h] -> gated residual update + AdaLN + H256 + INT8 -> W8A8 projection
+    [h -> n], with the gate in the previous GEMM's epilogue or in the fused preparation.  TOPS
+    counts both projections' MACs x 2, the reference's effective_tops."""
+    from m5kernels_amd import gate_chain, quantize
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    bf = torch.bfloat16
+
+    def arr(shape, factor=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * factor).to(bf)
+
+    aq, sa = quantize(arr((m, pk)), "int8")
+    q0, s0 = quantize(arr((h, pk), pk**-0.5), "int8")
+    q1, s1 = quantize(arr((n, h), h**-0.5), "int8")
+    residual, gate = arr((m, h)), arr((h,), 0.2)
+    gamma, scale, shift = (1 + 0.1 * torch.randn((h,), generator=g, device=dev)).to(bf), arr((h,), 0.2), arr((h,), 0.1)
+    signs = torch.ones(h, dtype=torch.int8, device=dev)
+    ops = 2.0 * m * h * (pk + n)
+    out = {"m": m, "k": h, "previous_k": pk, "n": n}
+    for placement in ("gate-in-gemm", "gate-in-norm"):
+        t = time_op(torch, lambda: gate_chain(aq, sa, q0, s0, q1, s1, residual, gate, gamma, scale, shift, signs,
+                                              placement=placement))
+        out[f"{placement}_ms"] = t["avg_ms"]
+        out[f"{placement}_TOPS"] = ops / (t["avg_ms"] * 1e-3) / 1e12
+    return out
+
+
 def _rms_case(torch, dev, m=4096, k=4096, block=256):
     """RMS scale-folded INT8 quantizer (rms_quantize) on a bf16 [m, k] activation, H256."""
     from m5kernels_amd import rms_quantize
@@ -310,6 +339,8 @@ def extras(torch, dev):
         ("qk_rope_m9914", lambda: _qk_case(torch, dev)),
         ("rms_quantize_m4096_h256", lambda: _rms_case(torch, dev)),
         ("grouped_qkv_m4096_h32", lambda: _qkv_case(torch, dev)),
+        ("gate_chain_attention_to_ffn_m4096", lambda: _chain_case(torch, dev)),
+        ("gate_chain_ffn_to_q_m4096", lambda: _chain_case(torch, dev, pk=14336, n=7168)),
     ]
     for name, fn in cases:
         log(f"[bench] extra {name}")

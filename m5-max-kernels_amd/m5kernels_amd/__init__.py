@@ -9,6 +9,7 @@ from .hip import gemm, gemm_i8_accumulators, quantize
 from .qk_rope import projection_qk_rope, projection_qkv_rope, qk_norm_rope
 from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
 from .rms_quant import rms_quantize
+from .chains import gate_chain
 from .norm_hadamard import (
     fused_gated_residual_norm_hadamard_quantize,
     fused_norm_hadamard_quantize,
@@ -31,4 +32,5 @@ __all__ = [
     "qk_norm_rope",
     "projection_qkv_rope",
     "rms_quantize",
+    "gate_chain",
 ]
