@@ -307,6 +307,57 @@ def _chain_case(torch, dev, m=4096, h=5376, pk=7168, n=14336):
     return out
 
 
+def _shift_split_case(torch, dev, m=4096, k=5376, n=7168):
+    """Shift-split Q projection (docs/affine-shift-splitting.md, P = 1): cached FP32 shift bias +
+    RMS-folded H256 INT8 + W8A8 with bias epilogue, against the full FP32 AdaLN fused prep +
+    W8A8; plus the conditioning-table build at P = 1, 3, 60, 117 rows (bias-cache study)."""
+    from m5kernels_amd import (fused_norm_hadamard_quantize, gemm, norm_shift_split_gemm, quantize, rotate,
+                               shift_split_condition)
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    bf = torch.bfloat16
+
+    def arr(shape, factor=1.0, offset=0.0):
+        return (offset + torch.randn(shape, generator=g, device=dev) * factor).to(bf)
+
+    x, w = arr((m, k)), arr((n, k))
+    gamma, scale, shift = arr((k,), 0.1, 1.0), arr((k,), 0.2), arr((k,), 0.1)
+    signs = torch.ones(k, dtype=torch.int8, device=dev)
+    wq, ws = quantize(rotate(w, 256, signs), "int8")
+    ops = 2.0 * m * n * k
+
+    def condition():
+        return shift_split_condition(gamma, scale, shift, w, bias_backend="mpp-bf16-to-fp32")
+
+    combined, bias = condition()
+
+    def split_online():
+        return norm_shift_split_gemm(x, wq, ws, signs, combined, bias)
+
+    def split_with_condition():
+        c, b = condition()
+        return norm_shift_split_gemm(x, wq, ws, signs, c, b)
+
+    def full_fp32():
+        q, s = fused_norm_hadamard_quantize(x, gamma, scale, shift, signs, 256, round_output="fp32")
+        return gemm(q, wq, "int8", a_scales=s, b_scales=ws, output_dtype=bf)
+
+    out = {"m": m, "k": k, "n": n}
+    for key, fn in (("split_cached_online", split_online), ("split_with_condition", split_with_condition),
+                    ("full_fp32_adaln_online", full_fp32), ("condition_prepare", condition)):
+        t = time_op(torch, fn)
+        out[f"{key}_ms"] = t["avg_ms"]
+        if key != "condition_prepare":
+            out[f"{key}_TOPS"] = ops / (t["avg_ms"] * 1e-3) / 1e12
+    wbytes = 2 * n * k
+    for p in (1, 3, 60, 117):
+        sc, sh = arr((p, k), 0.2), arr((p, k), 0.1)
+        t = time_op(torch, lambda: shift_split_condition(gamma, sc, sh, w, bias_backend="mpp-bf16-to-fp32"))
+        out[f"bias_cache_p{p}_ms"] = t["avg_ms"]
+        out[f"bias_cache_p{p}_weight_GBps"] = wbytes / (t["avg_ms"] * 1e-3) / 1e9
+    return out
+
+
 def _rms_case(torch, dev, m=4096, k=4096, block=256):
     """RMS scale-folded INT8 quantizer (rms_quantize) on a bf16 [m, k] activation, H256."""
     from m5kernels_amd import rms_quantize
@@ -341,6 +392,7 @@ def extras(torch, dev):
         ("grouped_qkv_m4096_h32", lambda: _qkv_case(torch, dev)),
         ("gate_chain_attention_to_ffn_m4096", lambda: _chain_case(torch, dev)),
         ("gate_chain_ffn_to_q_m4096", lambda: _chain_case(torch, dev, pk=14336, n=7168)),
+        ("shift_split_q_m4096", lambda: _shift_split_case(torch, dev)),
     ]
     for name, fn in cases:
         log(f"[bench] extra {name}")

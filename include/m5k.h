@@ -26,6 +26,8 @@
  *   projection_qk_rope       src/m5kernels/qk_rope.py:120-182
  *   qk_norm_rope             src/m5kernels/qk_rope.py:185-203
  *   rms_quantize             src/m5kernels/rms_quant.py:41-117
+ *   grouped QKV projection   integrations/h3/qkv_candidate.metal:1-20
+ *   shift-split conditioning src/m5kernels/norm_hadamard_gemm.py:233-247,459-460
  */
 #ifndef M5K_H
 #define M5K_H
@@ -243,6 +245,21 @@ int m5k_projection_qkv_rope(const void* a, const void* b, int ab_dtype, int64_t 
 int m5k_rms_quantize(const void* x, int x_dtype, int64_t rows, int64_t k, const float* gamma,
                      const int8_t* signs, int block, int fold_scale, float epsilon, int8_t* q,
                      float* scales, void* stream);
+
+/*
+ * Conditioning tables of the shift-split projection.  Replaces condition_prepare and
+ * bias_prepare of the norm-shift-split backend (src/m5kernels/norm_hadamard_gemm.py:233-247,
+ * 459-460).  gamma: [k]; scale, shift: [p_rows,k] (param_dtype and operand_dtype
+ * respectively; F32/F16/BF16); w: [n,k] original projection weights (operand_dtype).
+ * combined[p,j] = float(gamma[j]) * (1 + float(scale[p,j]))  FP32 [p_rows,k];
+ * bias[p,n] = sum_j float(shift[p,j]) * float(w[n,j])       FP32 [p_rows,n] (FP32
+ * accumulation; p_rows <= 8 one pass over w, more rows on the MFMA GEMM of m5k_gemm_float).
+ * The online projection is m5k_rms_quantize(x, combined[p], fold) followed by m5k_gemm_i8 with
+ * bias[p].
+ */
+int m5k_shift_split_condition(const void* gamma, const void* scale, int param_dtype,
+                              const void* shift, const void* w, int operand_dtype, int64_t p_rows,
+                              int64_t k, int64_t n, float* combined, float* bias, void* stream);
 
 #ifdef __cplusplus
 }

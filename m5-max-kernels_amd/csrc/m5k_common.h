@@ -84,6 +84,32 @@ constexpr int dtype_bytes() {
   return DT == M5K_F32 ? 4 : 2;
 }
 
+// Load 8 consecutive elements of dtype DT at element index e (16-byte aligned for 2-byte
+// types, 32-byte for FP32).
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t e, float (&v)[8]) {
+  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) + e * dtype_bytes<DT>());
+  if constexpr (DT == M5K_F32) {
+    const uint4 a = p[0], b = p[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+  } else {
+    const uint4 a = p[0];
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == M5K_BF16) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      } else {
+        v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
 // OCP FP8 E4M3 ("fn") encoder: nearest finite code, ties to even code,
 // saturating to 448 (code 126), sign taken from the sign bit.  Restates
 // numerics.fp8_encode (src/m5kernels/numerics.py:17-26) with exponent-field

@@ -53,32 +53,6 @@ struct PrepParams {
   int round_input;        // 1: O = XDT, 0: O = FP32
 };
 
-// Load 8 consecutive elements of dtype DT at element index e (16-byte aligned for 2-byte
-// types, 32-byte for FP32).
-template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t e, float (&v)[8]) {
-  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) + e * dtype_bytes<DT>());
-  if constexpr (DT == M5K_F32) {
-    const uint4 a = p[0], b = p[1];
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
-  } else {
-    const uint4 a = p[0];
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DT == M5K_BF16) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-      } else {
-        v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
-        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
-      }
-    }
-  }
-}
-
 // Round 8 values through dtype DT in place (the O(...) / R(...) cast) and return their
 // storage words; BF16 pairs take one v_cvt_pk_bf16_f32 each.
 template <int DT>

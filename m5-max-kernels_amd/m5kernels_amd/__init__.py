@@ -9,7 +9,7 @@ from .hip import gemm, gemm_i8_accumulators, quantize
 from .qk_rope import projection_qk_rope, projection_qkv_rope, qk_norm_rope
 from .hadamard import SUPPORTED_BLOCK_SIZES, rotate, rotate_quantize
 from .rms_quant import rms_quantize
-from .chains import gate_chain
+from .chains import gate_chain, norm_shift_split_gemm, shift_split_condition
 from .norm_hadamard import (
     fused_gated_residual_norm_hadamard_quantize,
     fused_norm_hadamard_quantize,
@@ -33,4 +33,6 @@ __all__ = [
     "projection_qkv_rope",
     "rms_quantize",
     "gate_chain",
+    "shift_split_condition",
+    "norm_shift_split_gemm",
 ]

@@ -37,6 +37,7 @@ SIGNATURES = {
     "m5k_quantize_rows": [_p, _i32, _i64, _i64, _i32, _p, _p, _p],
     "m5k_quantize_mxint8": [_p, _i32, _i64, _i64, _p, _p, _p],
     "m5k_rms_quantize": [_p, _i32, _i64, _i64, _p, _p, _i32, _i32, _f32, _p, _p, _p],
+    "m5k_shift_split_condition": [_p, _p, _i32, _p, _p, _i32, _i64, _i64, _i64, _p, _p, _p],
     "m5k_projection_qkv_rope": [_p, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _f32, _p, _p, _p, _p],
     "m5k_mxint8_to_bf16": [_p, _p, _i64, _i64, _p, _p],
     "m5k_gemm_i8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p],

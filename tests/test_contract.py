@@ -168,3 +168,32 @@ def test_grouped_qkv_validation():
                             cs, cs, "bf16")
     with pytest.raises(ValueError, match="ROCm device"):
         projection_qkv_rope(a, torch.zeros(384, 64, dtype=torch.bfloat16), g, g, cs, cs, "bf16")
+
+
+def test_shift_split_validation():
+    """norm_hadamard_gemm.py:39-44: the split policy needs RMS, round_output=fp32, one_read and a
+    known bias backend; the tables need matching shapes.  All raised before device work."""
+    from m5kernels_amd import norm_shift_split_gemm, shift_split_condition
+
+    x, s = torch.zeros(2, 256, dtype=torch.bfloat16), torch.ones(256, dtype=torch.int8)
+    wq, ws, c, b = torch.zeros(3, 256, dtype=torch.int8), torch.ones(3), torch.ones(256), torch.zeros(3)
+    with pytest.raises(NotImplementedError, match="round_output=fp32"):
+        norm_shift_split_gemm(x, wq, ws, s, c, b, round_output="input")
+    with pytest.raises(NotImplementedError, match="round_output=fp32"):
+        norm_shift_split_gemm(x, wq, ws, s, c, b, norm="layer")
+    with pytest.raises(NotImplementedError, match="passes=one_read"):
+        norm_shift_split_gemm(x, wq, ws, s, c, b, passes="two_read")
+    with pytest.raises(ValueError, match="ROCm device"):
+        norm_shift_split_gemm(x, wq, ws, s, c, b)
+    g = torch.ones(256, dtype=torch.bfloat16)
+    w = torch.zeros(3, 256, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="bias preparation backend"):
+        shift_split_condition(g, g, g, w, bias_backend="numpy")
+    with pytest.raises(ValueError, match="\\[K\\] or \\[P,K\\]"):
+        shift_split_condition(g, g, torch.ones(2, 256, dtype=torch.bfloat16), w)
+    with pytest.raises(ValueError, match="gamma must have shape"):
+        shift_split_condition(torch.ones(255, dtype=torch.bfloat16), g, g, w)
+    with pytest.raises(ValueError, match="bfloat16 shift"):
+        shift_split_condition(g, g, g.float(), w, bias_backend="mpp-bf16-to-fp32")
+    with pytest.raises(ValueError, match="ROCm device"):
+        shift_split_condition(g, g, g, w)

@@ -482,3 +482,55 @@ def test_rms_ties_zero_rows_and_epsilon():
     small, large = ref.rms_quantize_reference(x, g, block_size=8, eps=1e-8), ref.rms_quantize_reference(x, g, block_size=8, eps=1.0)
     np.testing.assert_array_equal(small["quantized"], large["quantized"])
     assert np.all(small["scales"] > large["scales"])
+
+
+# ---- shift splitting (docs/affine-shift-splitting.md; tests/test_affine_rewrites.py) -----------
+
+
+def test_shift_crosses_projection_before_rounding():
+    """test_affine_rewrites.py:9-17 against the oracle's norm: (norm(x) c + beta) W^T equals
+    r (x c) W^T + beta W^T, and the split RMS encoding's normalized rotation is exactly the
+    rotation of the modulated activation without its shift (norm_hadamard_gemm.py:330-352)."""
+    rng = np.random.default_rng(29)
+    x, w = rng.normal(size=(7, 256)), rng.normal(size=(11, 256))
+    gamma, scale, beta = rng.normal(size=(3, 256))
+    y = ref.norm_modulate_reference(x, gamma, scale, beta)
+    r = 1 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + 1e-5)
+    c = gamma * (1 + scale)
+    np.testing.assert_allclose(y @ w.T, r * ((x * c) @ w.T) + beta @ w.T, rtol=1e-12, atol=1e-12)
+    signs = ref.hadamard_signs(256, 0)
+    split = ref.rms_quantize_reference(x, c, signs, 128)
+    dynamic = ref.block_hadamard_reference(y - beta, 128, signs)
+    np.testing.assert_allclose(split["normalized_rotated"], dynamic, rtol=1e-12, atol=1e-12)
+    rotated_w = ref.block_hadamard_reference(w, 128, signs)
+    np.testing.assert_allclose(dynamic @ rotated_w.T + beta @ w.T, y @ w.T, rtol=1e-12, atol=1e-12)
+
+
+def test_bf16_boundary_prevents_constant_shift_compensation():
+    """test_affine_rewrites.py:20-25: the BF16 rounding correction depends on the activation."""
+    a = np.array([1, 1 + 1 / 128], np.float32)
+    correction = ref.bf16_round_f32(a + np.float32(1 / 256)) - a
+    np.testing.assert_array_equal(correction, [0, 1 / 128])
+
+
+def test_folding_gamma_into_weights_can_destroy_int8_quality():
+    """test_affine_rewrites.py:28-39 through the oracle's quantize / dequantize."""
+    x, gamma, w = np.array([[1, 1000]], np.float32), np.array([1000, 1], np.float32), np.ones((1, 2), np.float32)
+
+    def qdq(z):
+        return ref.dequantize(*ref.quantize_reference(z, "int8"), "int8")
+
+    np.testing.assert_array_equal(qdq(x * gamma) @ qdq(w).T, [[2000]])
+    np.testing.assert_array_equal(qdq(x) @ qdq(w * gamma).T, [[0]])
+
+
+def test_shift_split_quantization_can_amplify_cancellation_error():
+    """test_affine_rewrites.py:42-55."""
+    u, beta = np.array([[1, 1000]], np.float32), np.array([[-0.99, -1000]], np.float32)
+
+    def qdq(z):
+        return ref.dequantize(*ref.quantize_reference(z, "int8"), "int8")
+
+    target = u + beta
+    assert np.linalg.norm(qdq(target) - target) < 1e-6
+    assert np.linalg.norm(qdq(u) + beta - target) > 0.9
