@@ -1,0 +1,217 @@
+"""CPU tests of the experiment harness: workload schema, the harness's float64 check numerics
+against the pinned oracle, config validation, record gating and the CLI's argument handling.
+Nothing here touches a GPU (unsupported/invalid cases are rejected before device work)."""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from m5kernels_amd.harness import cli, engine, experiments, workloads
+from m5kernels_amd.harness import numerics as nx
+from oracle import reference as ref
+
+
+# ---- workloads (workloads.py:9-37) -------------------------------------------------------------
+
+
+def test_validate_rejects_bad_cases():
+    with pytest.raises(ValueError, match="nonempty id"):
+        workloads.validate({"id": "", "op": "gemm", "m": 1, "n": 1, "k": 1})
+    with pytest.raises(ValueError, match="k must be a positive integer"):
+        workloads.validate({"id": "a", "op": "gemm", "m": 1, "n": 1, "k": 0})
+    with pytest.raises(ValueError, match="previous_k"):
+        workloads.validate({"id": "a", "op": "gate_epilogue_chain", "m": 1, "n": 1, "k": 1, "previous_k": 1.5})
+    with pytest.raises(KeyError):
+        workloads.validate({"id": "a", "op": "conv", "m": 1})
+
+
+def test_load_suites_and_duplicates(tmp_path):
+    smoke = workloads.load("smoke")
+    assert {c["op"] for c in smoke["cases"]} >= {"gemm", "norm_hadamard_gemm", "gated_norm_hadamard_gemm",
+                                                 "rms_quant_gemm", "gate_epilogue_chain", "qk_rope"}
+    h3 = workloads.load("h3")["cases"]
+    assert len(h3) == 55
+    down = next(c for c in h3 if c["id"] == "h3.ffn_down.m4096")
+    assert (down["m"], down["n"], down["k"]) == (4096, 5376, 14336)
+    p = tmp_path / "dup.json"
+    p.write_text(json.dumps({"cases": [{"id": "x", "op": "gemm", "m": 1, "n": 1, "k": 1}] * 2}))
+    with pytest.raises(ValueError, match="duplicate"):
+        workloads.load(str(p))
+
+
+# ---- harness numerics against the pinned oracle -------------------------------------------------
+
+
+def test_metrics_and_sampling_match_oracle():
+    rng = np.random.default_rng(1)
+    a, r = rng.normal(size=(5, 7)), rng.normal(size=(5, 7))
+    assert nx.metrics(a, r) == ref.metrics(a, r)
+    assert nx.metrics(np.zeros(3), np.zeros(3))["cosine"] == 1.0
+    assert not nx.metrics([np.nan], [1.0])["finite"]
+    for n in (1, 7, 32, 33, 4096, 9914):
+        np.testing.assert_array_equal(nx.sample_indices(n), ref.sample_indices(n))
+
+
+@pytest.mark.parametrize("block", [1, 32, 128, 256])
+def test_block_hadamard_matches_oracle(block):
+    rng = np.random.default_rng(block)
+    x = rng.normal(size=(6, 1024))
+    signs = ref.hadamard_signs(1024, 7)
+    np.testing.assert_array_equal(nx.hadamard_signs(1024, 7), signs)
+    expected = x * signs if block == 1 else ref.block_hadamard_reference(x, block, signs)
+    np.testing.assert_allclose(nx.block_hadamard(x, block, signs), expected, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+def test_norm_modulate_matches_oracle(norm):
+    rng = np.random.default_rng(3)
+    x, g, s, b = rng.normal(size=(4, 64)), rng.normal(size=64), rng.normal(size=64), rng.normal(size=64)
+    np.testing.assert_allclose(nx.norm_modulate(x, g, s, b, norm=norm), ref.norm_modulate_reference(x, g, s, b, norm=norm),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_bf16_round_and_dequantize_match_oracle():
+    rng = np.random.default_rng(4)
+    v = np.concatenate([rng.normal(size=1000) * 10.0 ** rng.integers(-30, 30, 1000), [0.0, -0.0, 1 + 2**-8]])
+    np.testing.assert_array_equal(nx.bf16_round(v), ref.bf16_round_reference(v))
+    codes = np.arange(256, dtype=np.uint8)
+    finite = ~np.isnan(ref.fp8_decode(codes))
+    np.testing.assert_array_equal(nx.fp8_decode(codes)[finite], ref.fp8_decode(codes)[finite].astype(np.float64))
+    q = rng.integers(-127, 128, size=(3, 64)).astype(np.int8)
+    e = rng.integers(100, 150, size=(3, 2)).astype(np.uint8)
+    np.testing.assert_array_equal(nx.dequantize(q, e, "mxint8"), ref.dequantize(q, e, "mxint8"))
+    s = rng.random(3).astype(np.float32)
+    np.testing.assert_allclose(nx.dequantize(q, s, "int8"), ref.dequantize(q, s, "int8"), rtol=1e-7)
+
+
+def test_qk_rope_and_rms_match_oracle():
+    rng = np.random.default_rng(5)
+    proj = rng.normal(size=(5, 3, 128))
+    gamma, cos, sin = rng.normal(size=128), rng.normal(size=(5, 48)), rng.normal(size=(5, 48))
+    np.testing.assert_allclose(nx.qk_rope(proj, gamma, cos, sin, epsilon=1e-6),
+                               ref.qk_rope_reference(proj, gamma, cos, sin, epsilon=1e-6)["output"], rtol=0, atol=0)
+    x, g = rng.normal(size=(4, 512)), rng.normal(size=512)
+    signs = ref.hadamard_signs(512, 2)
+    mine, theirs = nx.rms_quantize(x, g, signs, 256), ref.rms_quantize_reference(x, g, signs, 256)
+    np.testing.assert_array_equal(mine["quantized"], theirs["quantized"])
+    np.testing.assert_allclose(mine["scales"], theirs["scales"], rtol=1e-12)
+    np.testing.assert_allclose(mine["normalized_rotated"], theirs["normalized_rotated"], rtol=1e-12, atol=1e-12)
+
+
+# ---- validation before device work ---------------------------------------------------------------
+
+
+def _rms_case(**extra):
+    return dict(id="r", op="rms_quant_gemm", m=3, n=17, k=256, **extra)
+
+
+def test_rms_config_validation():
+    with pytest.raises(NotImplementedError, match="rms-direct/rms-folded"):
+        experiments.validate_rms_config(_rms_case(), "mpp", "int8", "normal")
+    with pytest.raises(NotImplementedError, match="block_size 1 or 256"):
+        experiments.validate_rms_config(_rms_case(rms_quant={"block_size": 128}), "rms-direct", "int8", "normal")
+    with pytest.raises(NotImplementedError, match="unsupported rms_quant options"):
+        experiments.validate_rms_config(_rms_case(rms_quant={"norm": "layer"}), "rms-direct", "int8", "normal")
+    with pytest.raises(NotImplementedError, match="semantics options"):
+        experiments.validate_rms_config(_rms_case(shift=1), "rms-direct", "int8", "normal")
+    with pytest.raises(ValueError, match="epsilon"):
+        experiments.validate_rms_config(_rms_case(rms_quant={"epsilon": 1e-50}), "rms-folded", "int8", "normal")
+    cfg = experiments.validate_rms_config(_rms_case(rms_quant={"block_size": 256, "gamma": "random"}), "rms-folded",
+                                          "int8", "outliers")
+    assert cfg["block_size"] == 256 and cfg["threads"] == 256 and cfg["sign_seed"] is None
+
+
+def test_qk_config_validation():
+    c = dict(id="q", op="qk_rope", m=4, n=256, k=512)
+    assert experiments.validate_qk_config(c, "qk-fused", "int8", "normal", (32, 128, 4, 1))["rope_half"] == 48
+    with pytest.raises(NotImplementedError, match="complete 128-wide heads"):
+        experiments.validate_qk_config(dict(c, n=200), "qk-fused", "int8", "normal", (32, 128, 4, 1))
+    with pytest.raises(NotImplementedError, match="H256"):
+        experiments.validate_qk_config(dict(c, k=384), "qk-staged", "int8", "normal", (32, 128, 4, 1))
+    with pytest.raises(ValueError, match="rope_half"):
+        experiments.validate_qk_config(dict(c, rope_half=65), "qk-staged", "int8", "normal", (32, 128, 4, 1))
+    with pytest.raises(NotImplementedError, match="Q/K tile"):
+        experiments.validate_qk_config(c, "qk-staged", "int8", "normal", (64, 64, 2, 1))
+
+
+@pytest.mark.parametrize("fusion,reason", [({}, "round_output=fp32"),
+                                           ({"norm": "layer", "round_output": "fp32"}, "round_output=fp32"),
+                                           ({"round_output": "fp32", "passes": "two_read"}, "passes=one_read"),
+                                           ({"round_output": "fp32", "bias_backend": "numpy"}, "bias preparation")])
+def test_shift_split_rejections_are_unsupported_records(fusion, reason):
+    """test_shift_split_engine.py:40-61: incompatible contracts are rejected as unsupported."""
+    c = dict(id="split.reject", op="norm_hadamard_gemm", m=3, n=17, k=256, fusion=fusion)
+    r = engine.run_case(c, "norm-shift-split", "int8", warmup=1, repeat=3)
+    assert r["status"] == "unsupported" and reason in r["reason"]
+
+
+def test_out_of_scope_ops_are_unsupported():
+    for c in workloads.load("h3")["cases"]:
+        if c["op"] in ("attention", "rms_modulate", "swiglu"):
+            r = engine.run_case(c, "mlx", "bf16")
+            assert r["status"] == "unsupported" and "outside" in r["reason"]
+
+
+def _fake_prepare(passing_transform, actual_offset):
+    """A host-only experiment whose output misses `expected` by `actual_offset`."""
+    import torch
+
+    def prepare(c, backend, precision, seed, distribution, tile):
+        expected = np.ones((2, 2))
+        stages = {"online_activation_plus_gemm": lambda: torch.ones((2, 2), dtype=torch.float64)}
+        meta = dict(transform_pass=passing_transform, mac_operations=8)
+        return (lambda: torch.full((2, 2), 1.0 + actual_offset, dtype=torch.float64)), (lambda y: y.numpy()), \
+            expected, expected, stages, meta
+
+    return prepare
+
+
+@pytest.mark.parametrize("transform,offset", [(False, 0.0), (True, 0.5)])
+def test_incorrect_records_are_never_timed(monkeypatch, transform, offset):
+    monkeypatch.setitem(experiments.PREPARE, "gemm", _fake_prepare(transform, offset))
+    r = engine.run_case(dict(id="g", op="gemm", m=2, n=2, k=2), "mpp", "int8")
+    assert r["status"] == "incorrect"
+    assert "timing" not in r and "stages" not in r and "effective_tops" not in r
+
+
+# ---- CLI and report -------------------------------------------------------------------------------
+
+
+def test_cli_rejects_bad_arguments(capsys):
+    assert cli.main(["bench", "--output", "x.json", "--warmup", "0"]) == 2
+    assert cli.main(["bench", "--output", "x.json", "--tile", "64", "64", "40", "1"]) == 2
+    assert "error:" in capsys.readouterr().err
+    with pytest.raises(SystemExit):
+        cli.main(["tune"])  # --output is required
+
+
+def test_cli_shapes_prints_suite(capsys):
+    assert cli.main(["shapes", "--suite", "smoke"]) == 0
+    assert json.loads(capsys.readouterr().out)["cases"][0]["id"] == "smoke.gemm"
+
+
+def test_report_table(tmp_path, capsys):
+    doc = {"results": [
+        {"case": {"id": "a"}, "backend": "mpp", "precision": "int8", "status": "ok", "quality_pass": True,
+         "timing": {"median_ms": 1.5}, "stages": {"online_activation_plus_gemm": {"median_ms": 1.75}},
+         "effective_tops": 12.345, "quality_error": {"relative_l2": 0.01234},
+         "transform": {"block_size": 256, "implementation": "metal", "sign_seed": None}},
+        {"case": {"id": "b"}, "backend": "mlx", "precision": "bf16", "status": "unsupported", "reason": "x"},
+    ]}
+    p = tmp_path / "r.json"
+    p.write_text(json.dumps(doc))
+    assert cli.main(["report", str(p)]) == 0
+    out = capsys.readouterr().out.splitlines()
+    assert out[2] == "| a | mpp | int8 | H256 / metal / signs=None | 1.5000 | 1.7500 | 12.35 | 0.01234 | pass | ok |"
+    assert out[3] == "| b | mlx | bf16 | — | — | — | — | — | — | unsupported |"
+
+
+def test_write_result_never_replaces(tmp_path):
+    p = tmp_path / "out.json"
+    engine.write_result(p, {"a": 1})
+    with pytest.raises(FileExistsError):
+        engine.write_result(p, {"a": 2})
+    assert json.loads(p.read_text()) == {"a": 1}
