@@ -215,3 +215,43 @@ def test_write_result_never_replaces(tmp_path):
     with pytest.raises(FileExistsError):
         engine.write_result(p, {"a": 2})
     assert json.loads(p.read_text()) == {"a": 1}
+
+
+# ---- profiling summary (profile_report.py:37-60) ------------------------------------------------
+
+
+def _trace_rows(names_durations):
+    rows, t = [], 1000
+    for i, (name, dur) in enumerate(names_durations):
+        rows.append(dict(Kernel_Name=name, Start_Timestamp=str(t), End_Timestamp=str(t + dur), VGPR_Count="128",
+                         Accum_VGPR_Count="0", SGPR_Count="32", LDS_Block_Size="131072", Scratch_Size="0",
+                         Workgroup_Size_X="512", Grid_Size_X="131072", Dispatch_Id=str(i)))
+        t += dur + 10
+    return rows
+
+
+def test_profile_summary_counts_only_the_marked_calls():
+    from m5kernels_amd.harness import profile
+
+    spin = "void at::cuda::(anonymous namespace)::spin_kernel(long)"
+    rows = _trace_rows([("warmup_kernel", 5000), (spin, 100)] + [("quant", 2000), ("gemm", 8000)] * 3
+                       + [(spin, 100), ("after", 7)])
+    s = profile.summarize_trace(list(reversed(rows)), expect_dispatches=2, iterations=3)
+    assert s["dispatches"] == 6 and s["dispatches_per_iteration"] == 2
+    names = [k["kernel"] for k in s["kernels"]]
+    assert names == ["gemm", "quant"]
+    gemm = s["kernels"][0]
+    assert gemm["calls"] == 3 and gemm["mean_us"] == 8.0 and gemm["lds_bytes"] == 131072
+    assert abs(gemm["share_of_kernel_time"] - 0.8) < 1e-12
+    with pytest.raises(ValueError, match="expected 3 x 3"):
+        profile.summarize_trace(rows, expect_dispatches=3, iterations=3)
+    with pytest.raises(ValueError, match="boundary"):
+        profile.summarize_trace(rows[2:-2])
+
+
+def test_profile_cli_rejects_bad_arguments(capsys):
+    from m5kernels_amd.harness import profile
+
+    assert profile.main(["run", "--case", "x", "--iterations", "0", "--output", "o.json"]) == 2
+    with pytest.raises(SystemExit):
+        profile.main(["summarize"])
