@@ -384,6 +384,7 @@ int launch_fused(const PrepParams& p, int64_t rows, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(rows));
   if (per_thread <= 1) fused_prep_kernel<GroupRow, XDT, PDT, B, 1, GATED><<<grid, block, 0, st>>>(p, rows);
   else if (per_thread <= 2) fused_prep_kernel<GroupRow, XDT, PDT, B, 2, GATED><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 3) fused_prep_kernel<GroupRow, XDT, PDT, B, 3, GATED><<<grid, block, 0, st>>>(p, rows);
   else if (per_thread <= 4) fused_prep_kernel<GroupRow, XDT, PDT, B, 4, GATED><<<grid, block, 0, st>>>(p, rows);
   else if (per_thread <= 8) fused_prep_kernel<GroupRow, XDT, PDT, B, 8, GATED><<<grid, block, 0, st>>>(p, rows);
   else {
@@ -426,6 +427,7 @@ int launch_norm(const PrepParams& p, int64_t rows, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(rows));
   if (per_thread <= 1) norm_modulate_kernel<GroupRow, XDT, PDT, 1><<<grid, block, 0, st>>>(p, rows);
   else if (per_thread <= 2) norm_modulate_kernel<GroupRow, XDT, PDT, 2><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 3) norm_modulate_kernel<GroupRow, XDT, PDT, 3><<<grid, block, 0, st>>>(p, rows);
   else if (per_thread <= 4) norm_modulate_kernel<GroupRow, XDT, PDT, 4><<<grid, block, 0, st>>>(p, rows);
   else if (per_thread <= 8) norm_modulate_kernel<GroupRow, XDT, PDT, 8><<<grid, block, 0, st>>>(p, rows);
   else {

@@ -73,17 +73,18 @@ DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 @pytest.mark.parametrize("norm", ["rms", "layer"])
 @pytest.mark.parametrize("dtype", list(DT))
 @pytest.mark.parametrize("kind", ["normal", "zeros", "outliers"])
-def test_h3_width_full_output(norm, dtype, kind, device):
+@pytest.mark.parametrize("width", [5376, 6144])
+def test_h3_width_full_output(norm, dtype, kind, width, device):
     rng = np.random.default_rng(621)
-    x = rng.standard_normal((7, 5376), dtype=np.float32)
+    x = rng.standard_normal((7, width), dtype=np.float32)
     if kind == "zeros":
         x.fill(0)
     elif kind == "outliers":
         x[:, ::137] *= 100
-    gamma = rng.uniform(0.5, 1.5, size=5376).astype(np.float32)
-    scale = rng.uniform(-0.3, 0.3, size=5376).astype(np.float32)
-    shift = rng.uniform(-0.1, 0.1, size=5376).astype(np.float32)
-    signs = ref.hadamard_signs(5376, 29)
+    gamma = rng.uniform(0.5, 1.5, size=width).astype(np.float32)
+    scale = rng.uniform(-0.3, 0.3, size=width).astype(np.float32)
+    shift = rng.uniform(-0.1, 0.1, size=width).astype(np.float32)
+    signs = ref.hadamard_signs(width, 29)
     xt = torch.from_numpy(x).to(device).to(DT[dtype])
     args = [torch.from_numpy(t).to(device) for t in (gamma, scale, shift, signs)]
     q, s = fused_norm_hadamard_quantize(xt, *args, 256, norm=norm)
@@ -160,15 +161,17 @@ def test_row_map_tables(norm, device):
 
 @pytest.mark.parametrize("norm", ["rms", "layer"])
 @pytest.mark.parametrize("round_output", ["input", "fp32"])
-@pytest.mark.parametrize("block", [128, 256, 512])
-def test_fused_equals_staged_bitwise(norm, round_output, block, device):
+@pytest.mark.parametrize("block,width", [(128, 4096), (256, 4096), (512, 4096), (256, 5120), (128, 6144),
+                                         (256, 3072), (512, 7168)])
+def test_fused_equals_staged_bitwise(norm, round_output, block, width, device):
+    """Widths cover every register-chunk count of a lane: 1.5, 2, 2.5, 3, 3.5 chunks of 8."""
     rng = np.random.default_rng(71)
-    x = torch.from_numpy(rng.standard_normal((9, 4096), dtype=np.float32)).to(device).to(torch.bfloat16)
-    gamma = (1 + 0.1 * torch.randn(4096, device=device)).to(torch.bfloat16)
-    scale = (0.1 * torch.randn(2, 4096, device=device)).to(torch.bfloat16)
-    shift = (0.1 * torch.randn(2, 4096, device=device)).to(torch.bfloat16)
+    x = torch.from_numpy(rng.standard_normal((9, width), dtype=np.float32)).to(device).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(width, device=device)).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(2, width, device=device)).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(2, width, device=device)).to(torch.bfloat16)
     row_map = torch.tensor([0, 1] * 4 + [1], dtype=torch.int32, device=device)
-    signs = torch.from_numpy(ref.hadamard_signs(4096, 5)).to(device)
+    signs = torch.from_numpy(ref.hadamard_signs(width, 5)).to(device)
     q, s = fused_norm_hadamard_quantize(x, gamma, scale, shift, signs, block, norm=norm, round_output=round_output,
                                         row_map=row_map)
     y = unfused_norm(x, gamma, scale, shift, norm=norm, round_output=round_output, row_map=row_map)
