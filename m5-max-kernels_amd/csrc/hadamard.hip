@@ -98,6 +98,7 @@ int launch_rotate_quant(const void* x, int64_t rows, int64_t k, const int8_t* si
   const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
   if (per_thread <= 1) rotate_quant_kernel<DT, B, 1><<<grid, block, 0, st>>>(x, k, signs, q, s);
   else if (per_thread <= 2) rotate_quant_kernel<DT, B, 2><<<grid, block, 0, st>>>(x, k, signs, q, s);
+  else if (per_thread <= 3) rotate_quant_kernel<DT, B, 3><<<grid, block, 0, st>>>(x, k, signs, q, s);
   else if (per_thread <= 4) rotate_quant_kernel<DT, B, 4><<<grid, block, 0, st>>>(x, k, signs, q, s);
   else if (per_thread <= 8) rotate_quant_kernel<DT, B, 8><<<grid, block, 0, st>>>(x, k, signs, q, s);
   else {

@@ -177,6 +177,7 @@ int launch_block(const RmsParams& p, int64_t rows, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
   if (per_thread <= 1) rms_quant_block_kernel<XDT, B, 1, FOLD><<<grid, block, 0, st>>>(p);
   else if (per_thread <= 2) rms_quant_block_kernel<XDT, B, 2, FOLD><<<grid, block, 0, st>>>(p);
+  else if (per_thread <= 3) rms_quant_block_kernel<XDT, B, 3, FOLD><<<grid, block, 0, st>>>(p);
   else if (per_thread <= 4) rms_quant_block_kernel<XDT, B, 4, FOLD><<<grid, block, 0, st>>>(p);
   else if (per_thread <= 8) rms_quant_block_kernel<XDT, B, 8, FOLD><<<grid, block, 0, st>>>(p);
   else {

@@ -52,7 +52,7 @@ def test_rotate_ffn_down_shape(block, device):
 
 
 @pytest.mark.parametrize("block", [32, 128, 256, 1024])
-@pytest.mark.parametrize("shape", [(7, 5376 // 256 * 256), (3, 4096), (2, 16384), (5, 1024)])
+@pytest.mark.parametrize("shape", [(7, 5376 // 256 * 256), (3, 4096), (3, 6144), (2, 16384), (5, 1024)])
 def test_fused_rotate_quantize_equals_composition(block, shape, device):
     if shape[1] % block:
         pytest.skip("K not divisible by block")
