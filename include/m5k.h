@@ -115,6 +115,21 @@ int m5k_gemm_i8(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t 
                 void* stream);
 
 /*
+ * The same W8A8 linear as m5k_gemm_i8 for short M: each output tile is split over `splits`
+ * contiguous ranges of K (1..64), the raw INT32 partial tiles go to workspace[splits][m][n]
+ * (int32, caller-owned, at least splits*m*n elements), and a second kernel sums them in
+ * split order and applies the identical epilogue.  INT32 sums are exact, so c is bit-identical
+ * to m5k_gemm_i8's.  Needs k % 16 == 0, 16-byte aligned a/b, m*k and n*k < 2^31.  Same
+ * contract as metal.gemm(a, b, "int8", ...) (src/m5kernels/metal.py:158-269); the split is
+ * this library's schedule for few-tile shapes (one or two 256-row tile rows).
+ */
+int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                       const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                       const float* bias, const int32_t* bias_row_map, const void* residual,
+                       const void* gate, const int32_t* gate_row_map, int splits, int32_t* workspace,
+                       int64_t workspace_elems, void* stream);
+
+/*
  * Raw INT32 accumulators of the W8A8 GEMM (test hook for bit-exact parity):
  * acc[m,n] = sum_k a[m,k]*b[n,k].  Same kernel main loop as m5k_gemm_i8.
  */

@@ -273,9 +273,13 @@ __device__ __forceinline__ void zero_acc(AccTile<MODE, G>& acc) {
 // The barrier sits between the two MFMA groups, so its latency and the next stage's first
 // LDS reads overlap MFMAs already in flight.  FP8 (one 64-byte sub-step) splits its MFMAs
 // the same way by block rows and alternates the two fragment sets between stages.
+//
+// The loop covers the K slabs [kt_begin, kt_begin + kt_count) of 64 bytes; a split-K launch
+// gives each workgroup one such range (slabs past the range, like chunks past K, load zeros).
 template <int MODE, class G>
 __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int M,
-                                             int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc) {
+                                             int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc,
+                                             int64_t kt_begin, int64_t kt_count) {
   constexpr int SUB = Traits<MODE>::sub_steps;
   static_assert(SUB == 1 || SUB == 2, "stage holds one or two sub-steps");
   constexpr int FM = G::FM;
@@ -291,7 +295,6 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
 
   const int drow = wave * G::DMA_ROWS + (lane >> 2);  // row of DMA instruction 0
   const int dchunk = (lane & 3) ^ ((lane >> 4) & 3);  // logical chunk (same for every i)
-  const int64_t kt_count = (Kb + BKB - 1) / BKB;
   const int64_t kt_padded = (kt_count + NST - 1) / NST * NST;
 
   // Per-lane source offsets of each DMA instruction (kOob for rows past M / N).
@@ -303,9 +306,9 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
     b_base[i] = tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb + dchunk * 16) : kOob;
   }
   const uint32_t lds_row0 = static_cast<uint32_t>(uwave * G::DMA_ROWS * BKB);
-  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kt) {
-    const uint32_t kofs = static_cast<uint32_t>(kt * BKB);
-    const bool kin = static_cast<int64_t>(kofs) + dchunk * 16 < Kb;
+  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {  // kr: slab index relative to kt_begin
+    const uint32_t kofs = static_cast<uint32_t>((kt_begin + kr) * BKB);
+    const bool kin = kr < kt_count && static_cast<int64_t>(kofs) + dchunk * 16 < Kb;
     const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0;
 #pragma unroll
     for (int i = 0; i < G::DMA_INSTR; ++i) {

@@ -42,3 +42,34 @@ extern "C" int m5k_gemm_i8_acc(const int8_t* a, const int8_t* b, int64_t m, int6
   return launch<I8, M5K_I32, EPI_NONE, EPI_NONE, true>(a, b, m, n, k, p, as_stream(stream), name);
 }
 
+
+extern "C" int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                                  const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                                  const float* bias, const int32_t* bias_row_map, const void* residual,
+                                  const void* gate, const int32_t* gate_row_map, int splits, int32_t* workspace,
+                                  int64_t workspace_elems, void* stream) {
+  clear_error();
+  const char* name = "m5k_gemm_i8_splitk";
+  if (int rc = check_shape(m, n, k, name)) return rc;
+  M5K_REQUIRE(a && b && c && a_scales && b_scales && workspace, "%s: null operand, scale, output or workspace", name);
+  M5K_REQUIRE(k <= 133144, "%s: K=%lld exceeds the INT32 worst-case bound 133144", name, (long long)k);
+  M5K_REQUIRE(!bias_row_map || bias, "%s: bias_row_map requires bias", name);
+  M5K_REQUIRE((residual == nullptr) == (gate == nullptr), "%s: residual and gate go together", name);
+  M5K_REQUIRE(!gate_row_map || gate, "%s: gate_row_map requires gate", name);
+  M5K_REQUIRE(!(bias && residual), "%s: bias and gated residual cannot be combined", name);
+  M5K_REQUIRE(!residual || c_dtype == M5K_BF16, "%s: gated epilogue requires BF16 output", name);
+  M5K_REQUIRE(splits >= 1 && splits <= 64, "%s: splits=%d outside [1,64]", name, splits);
+  M5K_REQUIRE(k % 16 == 0 && aligned16(a) && aligned16(b) && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31),
+              "%s: split-K needs 16-byte aligned operands with K %% 16 == 0 and operands under 2 GiB", name);
+  M5K_REQUIRE(workspace_elems >= static_cast<int64_t>(splits) * m * n, "%s: workspace holds %lld INT32, needs %lld",
+              name, (long long)workspace_elems, (long long)(static_cast<int64_t>(splits) * m * n));
+  EpiParams p{a_scales, b_scales, c, bias, bias_row_map, static_cast<const uint16_t*>(residual),
+              static_cast<const uint16_t*>(gate), gate_row_map};
+  hipStream_t st = as_stream(stream);
+  switch (c_dtype) {
+    case M5K_BF16: return launch_i8_splitk<M5K_BF16>(a, b, m, n, k, p, splits, workspace, st, name);
+    case M5K_F16: return launch_i8_splitk<M5K_F16>(a, b, m, n, k, p, splits, workspace, st, name);
+    case M5K_F32: return launch_i8_splitk<M5K_F32>(a, b, m, n, k, p, splits, workspace, st, name);
+    default: set_error("%s: unsupported output dtype %d", name, c_dtype); return M5K_EINVAL;
+  }
+}

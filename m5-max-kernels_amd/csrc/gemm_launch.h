@@ -43,7 +43,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   AccTile<MODE, G> acc;
-  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, (Kb + BKB - 1) / BKB);
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
 
   auto scaled = [&](int m, int n, auto v) {
@@ -141,6 +141,95 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   else
     gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
   return launch_status(name);
+}
+
+// ---- Split-K W8A8 for short M ------------------------------------------------------------
+//
+// With few output tiles (M of one or two tile rows) the plain launch leaves most CUs idle
+// while its few workgroups stream the whole weight.  The split form gives each tile `splits`
+// workgroups, each over a contiguous range of K slabs, writing raw INT32 partial tiles to
+// workspace[s][M][N]; a second kernel sums the partials in split order (exact: INT32 sums of
+// a bounded dot product) and applies the same FP32 epilogue as gemm_kernel, so the output
+// is bit-identical to the plain launch.
+template <int MODE>
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_splitk_kernel(const uint8_t* __restrict__ A,
+                                                                             const uint8_t* __restrict__ B, int M,
+                                                                             int N, int64_t Kb, int splits,
+                                                                             int64_t slabs_per_split,
+                                                                             int32_t* __restrict__ partial) {
+  using G = KernelGrid;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int tile = static_cast<int>(blockIdx.x) / splits, s = static_cast<int>(blockIdx.x) % splits;
+  int tm, tn;
+  tile_coords(tile, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int64_t kt_total = (Kb + BKB - 1) / BKB;
+  const int64_t kt0 = s * slabs_per_split;
+  const int64_t kt1 = kt0 + slabs_per_split < kt_total ? kt0 + slabs_per_split : kt_total;
+  AccTile<MODE, G> acc;
+  mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, kt0, kt1 - kt0);
+  int32_t* out = partial + static_cast<int64_t>(s) * M * N;
+  for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
+    if (m < M && n < N) out[static_cast<int64_t>(m) * N + n] = v;
+  });
+}
+
+template <int OUT_DT, int BIAS, int GATE>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ partial, int splits, int M,
+                                                              int N, EpiParams p) {
+  const int64_t total = static_cast<int64_t>(M) * N;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * 256) {
+    int32_t v = 0;
+    for (int s = 0; s < splits; ++s) v += partial[s * total + idx];
+    const int m = static_cast<int>(idx / N), n = static_cast<int>(idx - static_cast<int64_t>(m) * N);
+    float value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
+    if constexpr (BIAS != EPI_NONE) {
+      const int64_t boff = BIAS == EPI_TABLE ? (int64_t)p.bias_map[m] * N : 0;
+      value = value + p.bias[boff + n];
+    }
+    if constexpr (GATE != EPI_NONE) {
+      const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;
+      const float branch = round_through<M5K_BF16>(value);
+      const float res = bf16_bits_to_f32(p.residual[idx]);
+      const float g = bf16_bits_to_f32(p.gate[goff + n]);
+      store_elem<M5K_BF16>(p.c, idx, res + branch * g);
+    } else {
+      store_elem<OUT_DT>(p.c, idx, value);
+    }
+  }
+}
+
+template <int OUT_DT, int BIAS, int GATE>
+int launch_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
+                  int splits, int32_t* workspace, hipStream_t st, const char* name) {
+  const int64_t kt_total = (k + BKB - 1) / BKB;
+  const int64_t per = (kt_total + splits - 1) / splits;
+  const int used = static_cast<int>((kt_total + per - 1) / per);  // no empty split
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  M5K_REQUIRE(tiles * used <= 0x7FFFFFFF, "%s: too many workgroups", name);
+  gemm_splitk_kernel<I8><<<dim3(static_cast<unsigned>(tiles * used)), dim3(KernelGrid::THREADS), 0, st>>>(
+      reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(b), (int)m, (int)n, k, used, per,
+      workspace);
+  if (int rc = launch_status(name)) return rc;
+  const int64_t blocks = (m * n + 255) / 256;
+  const unsigned grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+  splitk_epilogue_kernel<OUT_DT, BIAS, GATE><<<dim3(grid), dim3(256), 0, st>>>(workspace, used, (int)m, (int)n, p);
+  return launch_status(name);
+}
+
+template <int OUT_DT>
+int launch_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
+                     int splits, int32_t* workspace, hipStream_t st, const char* name) {
+  if (p.bias) {
+    return p.bias_map ? launch_splitk<OUT_DT, EPI_TABLE, EPI_NONE>(a, b, m, n, k, p, splits, workspace, st, name)
+                      : launch_splitk<OUT_DT, EPI_VECTOR, EPI_NONE>(a, b, m, n, k, p, splits, workspace, st, name);
+  }
+  if (p.residual) {
+    return p.gate_map ? launch_splitk<M5K_BF16, EPI_NONE, EPI_TABLE>(a, b, m, n, k, p, splits, workspace, st, name)
+                      : launch_splitk<M5K_BF16, EPI_NONE, EPI_VECTOR>(a, b, m, n, k, p, splits, workspace, st, name);
+  }
+  return launch_splitk<OUT_DT, EPI_NONE, EPI_NONE>(a, b, m, n, k, p, splits, workspace, st, name);
 }
 
 inline int check_shape(int64_t m, int64_t n, int64_t k, const char* name) {

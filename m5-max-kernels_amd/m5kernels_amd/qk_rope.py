@@ -18,6 +18,7 @@ from numbers import Integral, Real
 import torch
 
 from . import _lib
+from .hip import gemm, splitk_plan
 
 HEAD_DIM = 128
 
@@ -104,8 +105,14 @@ def projection_qk_rope(
             raise ValueError("INT8 requires float32 a_scales[M] and b_scales[N]")
     elif a_scales is not None or b_scales is not None:
         raise ValueError("BF16 projection does not accept quantization scales")
-    rope_half, epsilon = _validate_norm(m, n, gamma, cos, sin, epsilon)
+    rope_half, eps32 = _validate_norm(m, n, gamma, cos, sin, epsilon)
     _validate_tile(tile)
+    if mode == "int8" and splitk_plan(m, n, k) > 1:
+        # Few output tiles (short M): the split-K W8A8 projection to BF16, then the staged
+        # postprocess.  Both are the fused kernel's arithmetic, so the bits are the same.
+        projected = gemm(a, b, "int8", a_scales=a_scales, b_scales=b_scales, output_dtype=torch.bfloat16)
+        return qk_norm_rope(projected, gamma, cos, sin, epsilon=epsilon)
+    epsilon = eps32
     a = _lib.device_tensor(a, "a")
     b = _lib.device_tensor(b, "b")
     gamma, cos, sin = _tables(gamma, cos, sin)

@@ -250,3 +250,71 @@ def test_mxint8_gemm(shape, device):
     assert ref.metrics(np_of(y), a.double().cpu().numpy() @ w.double().cpu().numpy().T)["relative_l2"] < 0.05
     yb = gemm(aq, wq, "mxint8", a_scales=ae, b_scales=we, output_dtype=torch.bfloat16)
     assert yb.dtype == torch.bfloat16
+
+
+# ---- split-K W8A8 for short M (m5k_gemm_i8_splitk) -------------------------------------------
+
+
+def _gemm_i8_call(entry, a, b, sa, sb, out, *, splits=None, bias=None, bias_map=None, residual=None, gate=None,
+                  gate_map=None):
+    from m5kernels_amd import _lib
+
+    m, k = a.shape
+    n = b.shape[0]
+    c = torch.empty((m, n), dtype=out, device=a.device)
+    args = [_lib.ptr(a), _lib.ptr(b), m, n, k, _lib.ptr(sa), _lib.ptr(sb), _lib.ptr(c), _lib.dtype_code(c),
+            _lib.ptr(bias), _lib.ptr(bias_map), _lib.ptr(residual), _lib.ptr(gate), _lib.ptr(gate_map)]
+    if entry == "m5k_gemm_i8_splitk":
+        ws = torch.full((splits, m, n), 12345, dtype=torch.int32, device=a.device)  # stale contents must not leak
+        args += [splits, _lib.ptr(ws), ws.numel()]
+    _lib.call(entry, *args, _lib.stream_of(a))
+    return c
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 4096), (7, 33, 768), (128, 7168, 5376), (200, 1000, 2000),
+                                   (300, 520, 1024)])
+@pytest.mark.parametrize("splits", [2, 3, 7, 16])
+@pytest.mark.parametrize("epilogue", ["bf16", "fp32", "fp16", "bias", "bias_table", "gate", "gate_table"])
+def test_splitk_bit_identical_to_plain(shape, splits, epilogue, device):
+    """Split-K sums exact INT32 partials and applies the plain epilogue, so every output bit
+    matches m5k_gemm_i8 (K 2000 ends in a partial 64-byte slab; 16 splits of short K leave
+    some ranges shorter than a stage)."""
+    m, n, k = shape
+    g = torch.Generator(device="cpu").manual_seed(m + n + k + splits)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
+    sa = (torch.rand(m, generator=g) * 0.01 + 1e-3).to(device)
+    sb = (torch.rand(n, generator=g) * 0.01 + 1e-3).to(device)
+    kw, out = {}, {"fp32": torch.float32, "fp16": torch.float16}.get(epilogue, torch.bfloat16)
+    rows = torch.tensor([i % 3 for i in range(m)], dtype=torch.int32, device=device)
+    if epilogue.startswith("bias"):
+        kw["bias"] = torch.randn((3, n) if epilogue == "bias_table" else (n,), generator=g).to(device)
+        kw["bias_map"] = rows if epilogue == "bias_table" else None
+    elif epilogue.startswith("gate"):
+        kw["residual"] = torch.randn((m, n), generator=g).to(torch.bfloat16).to(device)
+        kw["gate"] = torch.randn((3, n) if epilogue == "gate_table" else (n,), generator=g).to(torch.bfloat16).to(device)
+        kw["gate_map"] = rows if epilogue == "gate_table" else None
+    plain = _gemm_i8_call("m5k_gemm_i8", a, b, sa, sb, out, **kw)
+    split = _gemm_i8_call("m5k_gemm_i8_splitk", a, b, sa, sb, out, splits=splits, **kw)
+    assert torch.equal(plain.view(torch.int16 if out != torch.float32 else torch.int32),
+                       split.view(torch.int16 if out != torch.float32 else torch.int32))
+
+
+def test_splitk_plan_and_routing(device):
+    """gemm() takes the split path for few-tile shapes and the plain one otherwise; both are
+    bit-exact against the oracle's W8A8 epilogue."""
+    from m5kernels_amd.hip import splitk_plan
+
+    assert splitk_plan(4096, 4096, 16384) == 1
+    assert splitk_plan(128, 7168, 5376) > 1 and splitk_plan(16, 4096, 4096) > 1
+    g = torch.Generator(device="cpu").manual_seed(3)
+    for m, n, k in ((128, 1536, 5376), (16, 4096, 4096)):
+        assert splitk_plan(m, n, k) > 1
+        a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
+        b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
+        sa = (torch.rand(m, generator=g) + 0.5).to(device)
+        sb = (torch.rand(n, generator=g) + 0.5).to(device)
+        y = gemm(a, b, "int8", a_scales=sa, b_scales=sb, output_dtype=torch.bfloat16)
+        acc = ref.c_gemm_i8_acc(np_of(a), np_of(b))
+        expected = ref.c_i8_epilogue(acc, np_of(sa), np_of(sb), out="bf16")
+        np.testing.assert_array_equal(bits_of(y), expected)

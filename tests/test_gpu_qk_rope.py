@@ -248,3 +248,24 @@ def test_grouped_qkv_equals_staged(mode, rope_half, m, heads, device):
         assert torch.equal(out, staged), f"stream {stream}"
     assert torch.equal(v, blocks[:, :, 2, :].permute(1, 0, 2).contiguous())
     assert q.shape == kk.shape == v.shape == (heads, m, 128)
+
+
+@pytest.mark.parametrize("m", [1, 17, 128, 200])
+def test_short_m_routing_matches_fused_kernel(m, device):
+    """Short-M INT8 projections take the split-K GEMM plus the staged postprocess; the result
+    equals the fused kernel's (called through the C ABI directly) bit for bit."""
+    from m5kernels_amd import _lib
+    from m5kernels_amd.hip import splitk_plan
+
+    n, k = 768, 5376
+    assert splitk_plan(m, n, k) > 1
+    rng = np.random.default_rng(m)
+    a, sa = quantize(torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device), "int8")
+    b, sb = quantize(torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device), "int8")
+    gamma, cos, sin = _tables(rng, m, device)
+    routed = projection_qk_rope(a, b, gamma, cos, sin, "int8", a_scales=sa, b_scales=sb, epsilon=1e-6)
+    fused = torch.empty((n // 128, m, 128), dtype=torch.bfloat16, device=device)
+    _lib.call("m5k_projection_qk_rope", _lib.ptr(a), _lib.ptr(b), _lib.dtype_code(a), m, n, k, _lib.ptr(sa),
+              _lib.ptr(sb), _lib.ptr(gamma.contiguous()), _lib.ptr(cos.contiguous()), _lib.ptr(sin.contiguous()),
+              cos.shape[1], float(np.float32(1e-6)), _lib.ptr(fused), _lib.stream_of(a))
+    np.testing.assert_array_equal(bits_of(routed), bits_of(fused))
