@@ -127,6 +127,7 @@ def _gemm_case(torch, dev, m, k, n, seed, mode="int8", outlier_every=None):
         "gemm_ms": only["avg_ms"],
         "gemm_TOPS": ops / (only["avg_ms"] * 1e-3) / 1e12,
         "gemm_frac_of_peak": ops / (only["avg_ms"] * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+        "gemm_weight_GBps": n * k / (only["avg_ms"] * 1e-3) / 1e9,  # the bound that matters at short M
         "online_p10_p90_ms": [step["p10_ms"], step["p90_ms"]],
     }
 
@@ -385,6 +386,8 @@ def extras(torch, dev):
         ("ffn_down_h128_int8_online", lambda: _hadamard_case(torch, dev)),
         ("q_proj_4096_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 4096, SEED)),
         ("ffn_up_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 16384, SEED)),
+        ("ffn_down_m128_int8_online_splitk", lambda: _gemm_case(torch, dev, 128, K, N, SEED)),
+        ("q_proj_m128_int8_online_splitk", lambda: _gemm_case(torch, dev, 128, 4096, 4096, SEED)),
         ("fused_prep_m4096", lambda: _prep_case(torch, dev, 4096)),
         ("fused_prep_m9914", lambda: _prep_case(torch, dev, 9914)),
         ("qk_rope_m9914", lambda: _qk_case(torch, dev)),
