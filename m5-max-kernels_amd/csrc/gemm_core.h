@@ -2,25 +2,28 @@
 // K-contiguous ("NT", the reference's weight layout [N,K], metal.py:72-73).
 //
 // Workgroup tile 256 x 256 with 8 wave64 in a 2 x 4 grid; each wave owns a 128 x 64
-// sub-tile.  K advances 64 bytes per stage; a stage is A[256 x 64 B] + B[256 x 64 B] =
-// 32 KiB of LDS in a ring of 4 stages (128 KiB of the 160 KiB per CU), filled by direct
-// global->LDS buffer loads issued 3 stages ahead.  LDS rows are 64 B with the 16-byte chunk
-// index XOR-swizzled by (row >> 2) & 3 (see swz()).
+// sub-tile.  K advances 128 bytes (one L2 line of every row) per stage; a stage is
+// A[256 x 128 B] + B[256 x 128 B] = 64 KiB of LDS, double-buffered (128 KiB of the 160 KiB
+// per CU) and filled by direct global->LDS buffer loads of whole rows issued one stage ahead.
+// LDS rows are 128 B with the 16-byte chunk index XOR-swizzled by (row >> 1) & 7 (see swz()).
+// Against 64-byte stages in a 4-deep ring this measured 6% (INT8) and 14% (BF16) faster at
+// K = 16384, where half-line requests cost a second trip to L2 for every line, and equal
+// elsewhere.
 //
-// MFMA blocks.  INT8, BF16 and FP16 use 16 x 16 blocks that take a whole 64-byte slab of K
-// per instruction (v_mfma_i32_16x16x64_i8, v_mfma_f32_16x16x32_{bf16,f16}): 8 x 4 blocks
-// per wave, 4 accumulator registers each.  FP8 (v_mfma_scale_f32_32x32x64_f8f6f4) and FP32
+// MFMA blocks.  INT8, BF16 and FP16 use 16 x 16 blocks that take 64 bytes of K per
+// instruction (v_mfma_i32_16x16x64_i8, v_mfma_f32_16x16x32_{bf16,f16}): 8 x 4 blocks per
+// wave, 4 accumulator registers each.  FP8 (v_mfma_scale_f32_32x32x64_f8f6f4) and FP32
 // (v_mfma_f32_32x32x2_f32) use 32 x 32 blocks: 4 x 2 per wave, 16 registers each.  The
 // 16 x 16 form measured ~5% faster than 32 x 32 on the FFN-down and 4096^3 shapes with the
 // same LDS traffic and MFMA cycles per slab.
 //
 // Operand layout.  16 x 16: lane l supplies row (l & 15) and the 16-byte K chunk (l >> 4)
-// of the slab.  32 x 32: row (l & 31) and chunk 2s + (l >> 5) of sub-step s (a 32-byte
-// slice for FP8; FP32 issues one K = 2 MFMA per float of the slice).  A and B use the same
-// K-slice mapping, so the products pair up correctly whatever order the hardware sums them
-// in (exact for INT32 accumulation).  Accumulator register r of lane l holds
-// C[(l >> 4) * 4 + r][l & 15] (16 x 16) or C[(r >> 2) * 8 + (l >> 5) * 4 + (r & 3)][l & 31]
-// (32 x 32).
+// of a 64-byte sub-step.  32 x 32: row (l & 31) and chunk 2s + (l >> 5) of 32-byte sub-step s
+// (FP32 issues one K = 2 MFMA per float of the chunk), or chunks 2(l >> 5), +1 of a 64-byte
+// sub-step (FP8).  A and B use the same K-slice mapping, so the products pair up correctly
+// whatever order the hardware sums them in (exact for INT32 accumulation).  Accumulator
+// register r of lane l holds C[(l >> 4) * 4 + r][l & 15] (16 x 16) or
+// C[(r >> 2) * 8 + (l >> 5) * 4 + (r & 3)][l & 31] (32 x 32).
 #pragma once
 
 #include <type_traits>
@@ -41,15 +44,15 @@ enum Mode { I8 = 0, F8 = 1, BF16 = 2, F16 = 3, F32 = 4 };
 
 constexpr int BM = 256;   // tile rows (A rows / C rows)
 constexpr int BN = 256;   // tile cols (B rows / C cols)
-constexpr int BKB = 64;   // K bytes per stage (LDS row length)
-constexpr int NST = 4;    // LDS stages in flight
+constexpr int BKB = 128;  // K bytes per stage (LDS row length, one L2 line)
+constexpr int NST = 2;    // LDS stage buffers
 constexpr int STAGE_BYTES = BM * BKB;  // one operand, one stage
 constexpr int GROUP_M = 4;             // tile-rows per raster band
 
 // Wave grid of a 256 x 256 tile.  WAVES_M x WAVES_N wave64, each owning a (256/WAVES_M) x
-// (256/WAVES_N) sub-tile of 32 x 32 MFMA blocks.  2 x 2 = one wave per SIMD with 256
-// accumulator registers; 2 x 4 = two waves per SIMD with 128 each, so one wave's MFMAs keep
-// the pipe busy while its sibling waits at a barrier.
+// (256/WAVES_N) sub-tile of MFMA blocks.  2 x 2 = one wave per SIMD with 256 accumulator
+// registers; 2 x 4 = two waves per SIMD with 128 each, so one wave's MFMAs keep the pipe busy
+// while its sibling waits at a barrier.
 template <int WAVES_M_, int WAVES_N_>
 struct Grid {
   static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
@@ -57,8 +60,8 @@ struct Grid {
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int FM = WM / 32, FN = WN / 32;
-  static constexpr int DMA_ROWS = BM / WAVES;      // rows of each operand one wave DMAs per stage
-  static constexpr int DMA_INSTR = DMA_ROWS / 16;  // 1 KiB (16 rows of 64 B) per instruction
+  static constexpr int DMA_ROWS = BM / WAVES;     // rows of each operand one wave DMAs per stage
+  static constexpr int DMA_INSTR = DMA_ROWS / 8;  // 1 KiB (8 rows of 128 B) per instruction
 };
 using Grid4 = Grid<2, 2>;
 using Grid8 = Grid<2, 4>;
@@ -69,14 +72,14 @@ struct Traits {
   using acc_t = v4f;
   static constexpr int MD = 16;
   static constexpr int elem_bytes = 2;
-  static constexpr int sub_steps = 1;  // 64 K-bytes per 16x16 MFMA
+  static constexpr int sub_steps = BKB / 64;  // 64 K-bytes per 16x16 MFMA
 };
 template <>
 struct Traits<I8> {
   using acc_t = v4i;
   static constexpr int MD = 16;
   static constexpr int elem_bytes = 1;
-  static constexpr int sub_steps = 1;
+  static constexpr int sub_steps = BKB / 64;
 };
 template <>
 struct Traits<F32> {
@@ -147,13 +150,13 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tn = inner / h;
 }
 
-// LDS layout of one operand stage: 256 rows x 64 bytes; the 16-byte chunk c of row r sits at
-// physical chunk c ^ ((r >> 2) & 3).  gfx950 serves ds_read_b128 16 lanes at a time over 64
-// banks (256 B); a fragment read covers 16 consecutive rows with one logical chunk, which
-// this swizzle spreads over all 16 bank groups (measured conflict-free on MI355X).
-__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+// LDS layout of one operand stage: 256 rows x 128 bytes (one L2 line per row); the 16-byte
+// chunk c of row r sits at physical chunk c ^ ((r >> 1) & 7).  gfx950 serves ds_read_b128 16
+// lanes at a time over 64 banks (256 B); a fragment read covers 16 consecutive rows with one
+// logical chunk, which lands on 16 distinct (row parity, physical chunk) bank groups.
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
-// All LDS of a GEMM kernel: NST stages x (A, B) x 16 KiB = 128 KiB.  The main loop uses it as
+// All LDS of a GEMM kernel: NST stages x (A, B) x 32 KiB = 128 KiB.  The main loop uses it as
 // the stage ring; epilogues may reuse it afterwards (e.g. as a 256 x 256 BF16 tile).  The DMA
 // writes are inline asm with "memory" clobbers and every consumer sits behind an explicit
 // wait and barrier, so one array serves all stages.
@@ -226,30 +229,32 @@ struct FragSet {
   Frag<MODE> b[Blk<MODE, G>::FN];
 };
 
-// Lane l reads row (l & 15) of each 16-row block at chunk (l >> 4) (16 x 16 MFMAs, one
-// sub-step per stage), row (l & 31) of each 32-row block at chunk 2s + (l >> 5) (16 bytes),
-// or chunks 2(l >> 5), +1 (32 bytes, FP8, one sub-step per stage).
+// Fragments of sub-step s.  16 x 16 blocks: lane l reads row (l & 15) of each block at
+// logical chunk 4s + (l >> 4) (64-byte sub-steps).  FP8: row (l & 31), chunks 4s + 2(l >> 5)
+// and the next one (64-byte sub-steps, 32 bytes a lane).  FP32: row (l & 31), chunk
+// 2s + (l >> 5) (32-byte sub-steps).  `fq` is the lane's chunk term (l >> 4, 2(l >> 5) or
+// l >> 5), `fsw` the swizzle of its row, which a block offset of 16 or 32 rows leaves alone.
 template <int MODE, class G>
 __device__ __forceinline__ void read_frags(const uint8_t* sa, const uint8_t* sb, int s, int a_row0, int b_row0,
-                                           int fhalf, int fsw, FragSet<MODE, G>& f) {
+                                           int fq, int fsw, FragSet<MODE, G>& f) {
+  constexpr int MD = Blk<MODE, G>::MD;
   if constexpr (MODE == F8) {
-    const int c0 = fhalf * 2;
+    const int c0 = 4 * s + fq;
     const int o0 = (c0 ^ fsw) << 4, o1 = ((c0 + 1) ^ fsw) << 4;
 #pragma unroll
-    for (int i = 0; i < G::FM; ++i) {
-      const uint8_t* p = sa + (a_row0 + 32 * i) * BKB;
+    for (int i = 0; i < Blk<MODE, G>::FM; ++i) {
+      const uint8_t* p = sa + (a_row0 + MD * i) * BKB;
       f.a[i].lo = *reinterpret_cast<const v4i*>(p + o0);
       f.a[i].hi = *reinterpret_cast<const v4i*>(p + o1);
     }
 #pragma unroll
-    for (int j = 0; j < G::FN; ++j) {
-      const uint8_t* p = sb + (b_row0 + 32 * j) * BKB;
+    for (int j = 0; j < Blk<MODE, G>::FN; ++j) {
+      const uint8_t* p = sb + (b_row0 + MD * j) * BKB;
       f.b[j].lo = *reinterpret_cast<const v4i*>(p + o0);
       f.b[j].hi = *reinterpret_cast<const v4i*>(p + o1);
     }
   } else {
-    constexpr int MD = Blk<MODE, G>::MD;
-    const int o = (MD == 32 ? ((s * 2 + fhalf) ^ fsw) : (fhalf ^ fsw)) << 4;
+    const int o = (((MODE == F32 ? 2 : 4) * s + fq) ^ fsw) << 4;
 #pragma unroll
     for (int i = 0; i < Blk<MODE, G>::FM; ++i)
       f.a[i].lo = *reinterpret_cast<const v4i*>(sa + (a_row0 + MD * i) * BKB + o);
@@ -279,30 +284,47 @@ __device__ __forceinline__ void zero_acc(AccTile<MODE, G>& acc) {
     for (int j = 0; j < Blk<MODE, G>::FN; ++j) acc[i][j] = typename Traits<MODE>::acc_t{};
 }
 
+// Lane constants of the fragment reads: (row in block, chunk term, row swizzle).
+template <int MODE>
+__device__ __forceinline__ void frag_lane(int lane, int& frow, int& fq, int& fsw) {
+  if constexpr (Traits<MODE>::MD == 16) {
+    frow = lane & 15;
+    fq = lane >> 4;
+  } else {
+    frow = lane & 31;
+    fq = MODE == F8 ? 2 * (lane >> 5) : lane >> 5;
+  }
+  fsw = swz(frow);
+}
+
+// Number of 128-byte K stages of a row of Kb bytes.
+__host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 1) / BKB; }
+
 // Direct-to-LDS main loop (rows 16-byte multiples, bases 16-byte aligned, operands < 2 GiB).
 //
 // DMA: per stage each wave moves DMA_ROWS rows of both operand tiles with DMA_INSTR + DMA_INSTR
-// buffer loads of 1 KiB (lane l -> row 16i + l/4, physical chunk l & 3, i.e. logical chunk
-// (l & 3) ^ ((l >> 4) & 3)).  Rows past M/N and chunks past K read as zero through
-// out-of-range buffer offsets.  Stage k+3 is requested while stage k is computed.
+// buffer loads of 1 KiB: lane l -> row 8i + l/8, physical chunk l & 7, i.e. whole 128-byte
+// rows, so both halves of an L2 line are requested by one instruction.  Rows past M/N and
+// chunks past K read as zero through out-of-range buffer offsets.
 //
-// Per stage (one wave, I8/BF16/F16: two 32-byte sub-steps):
-//   read sub-step 1 fragments | MFMAs of sub-step 0
-//   wait for own stage k+1 loads; barrier   (stage k+1 visible; stage k-1 buffer free)
-//   DMA stage k+3 into the freed buffer
-//   read stage k+1 sub-step 0 fragments | MFMAs of sub-step 1
-// The barrier sits between the two MFMA groups, so its latency and the next stage's first
-// LDS reads overlap MFMAs already in flight.  FP8 (one 64-byte sub-step) splits its MFMAs
-// the same way by block rows and alternates the two fragment sets between stages.
+// Two stage buffers.  Per stage kt (buffer kt & 1, SUB sub-steps):
+//   read sub-step s+1 fragments | MFMAs of sub-step s            (s < SUB - 1)
+//   MFMAs of the last sub-step, first half of the block rows
+//   wait for own stage kt+1 loads and all LDS reads; barrier  (stage kt+1 visible, buffer free)
+//   DMA stage kt+2 into buffer kt & 1
+//   read stage kt+1 sub-step 0 fragments | MFMAs of the last sub-step, second half
+// Stage kt+1's loads therefore have one whole stage to land, and the barrier sits between MFMA
+// groups, so its latency and the next stage's first LDS reads overlap MFMAs in flight.  Each
+// accumulator sees K in order, sub-step by sub-step.
 //
-// The loop covers the K slabs [kt_begin, kt_begin + kt_count) of 64 bytes; a split-K launch
-// gives each workgroup one such range (slabs past the range, like chunks past K, load zeros).
+// The loop covers the 128-byte K stages [kt_begin, kt_begin + kt_count); a split-K launch
+// gives each workgroup one such range (stages past the range, like chunks past K, load zeros).
 template <int MODE, class G>
 __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int M,
                                              int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc,
                                              int64_t kt_begin, int64_t kt_count) {
   constexpr int SUB = Traits<MODE>::sub_steps;
-  static_assert(SUB == 1 || SUB == 2, "stage holds one or two sub-steps");
+  static_assert(SUB % 2 == 0, "the last sub-step of a stage uses the second fragment set");
   constexpr int FM = Blk<MODE, G>::FM;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -314,77 +336,67 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   constexpr uint32_t kOob = 0x80000000u;  // beyond num_records: the load returns zeros
   const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform copy for LDS bases
 
-  const int drow = wave * G::DMA_ROWS + (lane >> 2);  // row of DMA instruction 0
-  const int dchunk = (lane & 3) ^ ((lane >> 4) & 3);  // logical chunk (same for every i)
-  const int64_t kt_padded = (kt_count + NST - 1) / NST * NST;
-
-  // Per-lane source offsets of each DMA instruction (kOob for rows past M / N).
+  // Per-lane source offsets of each DMA instruction (kOob for rows past M / N) and the byte
+  // offset of the logical chunk the lane moves.  Instruction i covers rows
+  // wave * DMA_ROWS + 8i + [0, 8) (DMA_ROWS a multiple of 16), whose swizzle is
+  // 4 (i & 1) + (l >> 4): the chunk offset depends on the parity of i only.
+  static_assert(G::DMA_ROWS % 16 == 0, "DMA row groups start at even row pairs");
+  const uint32_t lchunk[2] = {static_cast<uint32_t>(((lane & 7) ^ (lane >> 4)) << 4),
+                              static_cast<uint32_t>(((lane & 7) ^ (4 + (lane >> 4))) << 4)};
   uint32_t a_base[G::DMA_INSTR], b_base[G::DMA_INSTR];
 #pragma unroll
   for (int i = 0; i < G::DMA_INSTR; ++i) {
-    const int r = drow + 16 * i;
-    a_base[i] = tile_m0 + r < M ? static_cast<uint32_t>((int64_t)(tile_m0 + r) * Kb + dchunk * 16) : kOob;
-    b_base[i] = tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb + dchunk * 16) : kOob;
+    const int r = wave * G::DMA_ROWS + 8 * i + (lane >> 3);
+    a_base[i] = tile_m0 + r < M ? static_cast<uint32_t>((int64_t)(tile_m0 + r) * Kb) + lchunk[i & 1] : kOob;
+    b_base[i] = tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb) + lchunk[i & 1] : kOob;
   }
   const uint32_t lds_row0 = static_cast<uint32_t>(uwave * G::DMA_ROWS * BKB);
-  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {  // kr: slab index relative to kt_begin
+  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {  // kr: stage index relative to kt_begin
     const uint32_t kofs = static_cast<uint32_t>((kt_begin + kr) * BKB);
-    const bool kin = kr < kt_count && static_cast<int64_t>(kofs) + dchunk * 16 < Kb;
+    const bool live = kr < kt_count;
     const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0;
 #pragma unroll
     for (int i = 0; i < G::DMA_INSTR; ++i) {
-      dma16(la + 16 * i * BKB, (kin && a_base[i] != kOob) ? a_base[i] + kofs : kOob, rsrc_a);
-      dma16(lb + 16 * i * BKB, (kin && b_base[i] != kOob) ? b_base[i] + kofs : kOob, rsrc_b);
+      const bool kin = live && static_cast<int64_t>(kofs) + lchunk[i & 1] < Kb;
+      dma16(la + 8 * i * BKB, (kin && a_base[i] != kOob) ? a_base[i] + kofs : kOob, rsrc_a);
+      dma16(lb + 8 * i * BKB, (kin && b_base[i] != kOob) ? b_base[i] + kofs : kOob, rsrc_b);
     }
   };
 
-  constexpr int MDIM = Traits<MODE>::MD;
-  const int frow = MDIM == 32 ? (lane & 31) : (lane & 15), fhalf = MDIM == 32 ? (lane >> 5) : (lane >> 4),
-            fsw = swz(frow);
+  int frow, fq, fsw;
+  frag_lane<MODE>(lane, frow, fq, fsw);
   const int a_row0 = wm * G::WM + frow, b_row0 = wn * G::WN + frow;
 
   FragSet<MODE, G> f0, f1;
 
-  // One stage: buffer CUR, DMA target FREE (= stage k+3), next buffer NXT.  For FP8 the
-  // current fragments live in f0 on even stages and f1 on odd ones (P selects).
-  auto stage = [&](auto cur_tag, auto nxt_tag, auto free_tag, auto parity_tag, int64_t kt) {
-    constexpr int CUR = decltype(cur_tag)::value, NXT = decltype(nxt_tag)::value;
-    constexpr int FREE = decltype(free_tag)::value, P = decltype(parity_tag)::value;
-    if constexpr (SUB == 2) {
-      read_frags<MODE, G>(stage_a<CUR>(), stage_b<CUR>(), 1, a_row0, b_row0, fhalf, fsw, f1);
-      mfma_rows<MODE, G, 0, FM>(acc, f0);
-      wait_stage<2 * G::DMA_INSTR>();
-      stage_barrier();
-      dma(stage_a<FREE>(), stage_b<FREE>(), kt + 3);
-      read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fhalf, fsw, f0);
-      mfma_rows<MODE, G, 0, FM>(acc, f1);
-    } else {
-      FragSet<MODE, G>& fc = P ? f1 : f0;
-      FragSet<MODE, G>& fn = P ? f0 : f1;
-      mfma_rows<MODE, G, 0, FM / 2>(acc, fc);
-      wait_stage<2 * G::DMA_INSTR>();
-      stage_barrier();
-      dma(stage_a<FREE>(), stage_b<FREE>(), kt + 3);
-      read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fhalf, fsw, fn);
-      mfma_rows<MODE, G, FM / 2, FM>(acc, fc);
+  auto stage = [&](auto cur_tag, int64_t kt) {
+    constexpr int CUR = decltype(cur_tag)::value, NXT = CUR ^ 1;
+#pragma unroll
+    for (int s = 0; s + 1 < SUB; ++s) {
+      read_frags<MODE, G>(stage_a<CUR>(), stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw, (s & 1) ? f0 : f1);
+      mfma_rows<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0);
     }
+    mfma_rows<MODE, G, 0, FM / 2>(acc, f1);
+    wait_stage<0>();
+    // The DMA below overwrites this buffer: every wave's reads of it must have returned.
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stage_barrier();
+    dma(stage_a<CUR>(), stage_b<CUR>(), kt + 2);
+    read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw, f0);
+    mfma_rows<MODE, G, FM / 2, FM>(acc, f1);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
 
   dma(stage_a<0>(), stage_b<0>(), 0);
   dma(stage_a<1>(), stage_b<1>(), 1);
-  dma(stage_a<2>(), stage_b<2>(), 2);
-  wait_stage<4 * G::DMA_INSTR>();  // stage 0 landed (own loads)
+  wait_stage<2 * G::DMA_INSTR>();  // stage 0 landed (own loads)
   stage_barrier();
-  read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fhalf, fsw, f0);
-  for (int64_t kt = 0; kt < kt_padded; kt += NST) {
-    stage(I0{}, I1{}, I3{}, I0{}, kt);
-    stage(I1{}, I2{}, I0{}, I1{}, kt + 1);
-    stage(I2{}, I3{}, I1{}, I0{}, kt + 2);
-    stage(I3{}, I0{}, I2{}, I1{}, kt + 3);
+  read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fq, fsw, f0);
+  const int64_t kt_padded = (kt_count + 1) / 2 * 2;
+  for (int64_t kt = 0; kt < kt_padded; kt += 2) {
+    stage(I0{}, kt);
+    stage(I1{}, kt + 1);
   }
   // Drain the trailing (zero) DMAs before the LDS is reused or the wave exits.
   wait_stage<0>();
@@ -397,16 +409,16 @@ template <int MODE, class G>
 __device__ __forceinline__ void mainloop_staged(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int M,
                                                 int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc) {
   constexpr int SUB = Traits<MODE>::sub_steps;
+  constexpr int CHUNKS = BKB / 16;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
   zero_acc<MODE, G>(acc);
-  constexpr int ROWS_PER_PASS = G::THREADS / 4;  // chunk (t & 3) of rows (t >> 2) + pass * ROWS_PER_PASS
-  const int lc = tid & 3, lr = tid >> 2;
-  const int64_t kt_count = (Kb + BKB - 1) / BKB;
-  constexpr int MDIM = Traits<MODE>::MD;
-  const int frow = MDIM == 32 ? (lane & 31) : (lane & 15), fhalf = MDIM == 32 ? (lane >> 5) : (lane >> 4),
-            fsw = swz(frow);
+  constexpr int ROWS_PER_PASS = G::THREADS / CHUNKS;  // chunk (t % CHUNKS) of rows t / CHUNKS + pass * ROWS_PER_PASS
+  const int lc = tid % CHUNKS, lr = tid / CHUNKS;
+  const int64_t kt_count = k_stages(Kb);
+  int frow, fq, fsw;
+  frag_lane<MODE>(lane, frow, fq, fsw);
   const int a_row0 = wm * G::WM + frow, b_row0 = wn * G::WN + frow;
   for (int64_t kt = 0; kt < kt_count; ++kt) {
     const int64_t kb = kt * BKB + lc * 16;
@@ -429,7 +441,7 @@ __device__ __forceinline__ void mainloop_staged(const uint8_t* __restrict__ A, c
 #pragma unroll
     for (int s = 0; s < SUB; ++s) {
       FragSet<MODE, G> f;
-      read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), s, a_row0, b_row0, fhalf, fsw, f);
+      read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), s, a_row0, b_row0, fq, fsw, f);
       mfma_rows<MODE, G, 0, Blk<MODE, G>::FM>(acc, f);
     }
     __syncthreads();

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   AccTile<MODE, G> acc;
-  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, (Kb + BKB - 1) / BKB);
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
 
   auto scaled = [&](int m, int n, auto v) {
@@ -147,7 +147,7 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
 //
 // With few output tiles (M of one or two tile rows) the plain launch leaves most CUs idle
 // while its few workgroups stream the whole weight.  The split form gives each tile `splits`
-// workgroups, each over a contiguous range of K slabs, writing raw INT32 partial tiles to
+// workgroups, each over a contiguous range of 128-byte K stages, writing raw INT32 partial tiles to
 // workspace[s][M][N]; a second kernel sums the partials in split order (exact: INT32 sums of
 // a bounded dot product) and applies the same FP32 epilogue as gemm_kernel, so the output
 // is bit-identical to the plain launch.
@@ -155,7 +155,7 @@ template <int MODE>
 __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_splitk_kernel(const uint8_t* __restrict__ A,
                                                                              const uint8_t* __restrict__ B, int M,
                                                                              int N, int64_t Kb, int splits,
-                                                                             int64_t slabs_per_split,
+                                                                             int64_t stages_per_split,
                                                                              int32_t* __restrict__ partial) {
   using G = KernelGrid;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -163,9 +163,9 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_splitk_kernel(con
   int tm, tn;
   tile_coords(tile, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int64_t kt_total = (Kb + BKB - 1) / BKB;
-  const int64_t kt0 = s * slabs_per_split;
-  const int64_t kt1 = kt0 + slabs_per_split < kt_total ? kt0 + slabs_per_split : kt_total;
+  const int64_t kt_total = k_stages(Kb);
+  const int64_t kt0 = s * stages_per_split;
+  const int64_t kt1 = kt0 + stages_per_split < kt_total ? kt0 + stages_per_split : kt_total;
   AccTile<MODE, G> acc;
   mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, kt0, kt1 - kt0);
   int32_t* out = partial + static_cast<int64_t>(s) * M * N;
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __r
 template <int OUT_DT, int BIAS, int GATE>
 int launch_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
                   int splits, int32_t* workspace, hipStream_t st, const char* name) {
-  const int64_t kt_total = (k + BKB - 1) / BKB;
+  const int64_t kt_total = k_stages(k);
   const int64_t per = (kt_total + splits - 1) / splits;
   const int used = static_cast<int>((kt_total + per - 1) / per);  // no empty split
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
