@@ -6,9 +6,9 @@
 // A[256 x 128 B] + B[256 x 128 B] = 64 KiB of LDS, double-buffered (128 KiB of the 160 KiB
 // per CU) and filled by direct global->LDS buffer loads of whole rows issued one stage ahead.
 // LDS rows are 128 B with the 16-byte chunk index XOR-swizzled by (row >> 1) & 7 (see swz()).
-// Against 64-byte stages in a 4-deep ring this measured 6% (INT8) and 14% (BF16) faster at
-// K = 16384, where half-line requests cost a second trip to L2 for every line, and equal
-// elsewhere.
+// Against 64-byte stages in a 4-deep ring (half-line requests, one barrier per 64 bytes) this
+// measured 6-10% (INT8) and 12-14% (BF16) faster at K = 16384 and 1-5% faster elsewhere,
+// with bit-identical results.
 //
 // MFMA blocks.  INT8, BF16 and FP16 use 16 x 16 blocks that take 64 bytes of K per
 // instruction (v_mfma_i32_16x16x64_i8, v_mfma_f32_16x16x32_{bf16,f16}): 8 x 4 blocks per
