@@ -297,6 +297,44 @@ __device__ __forceinline__ void frag_lane(int lane, int& frow, int& fq, int& fsw
   fsw = swz(frow);
 }
 
+// One operand fragment of sub-step s (the per-mode chunk mapping of read_frags).
+template <int MODE>
+__device__ __forceinline__ void read_frag(const uint8_t* row, int s, int fq, int fsw, Frag<MODE>& f) {
+  if constexpr (MODE == F8) {
+    const int c0 = 4 * s + fq;
+    f.lo = *reinterpret_cast<const v4i*>(row + ((c0 ^ fsw) << 4));
+    f.hi = *reinterpret_cast<const v4i*>(row + (((c0 + 1) ^ fsw) << 4));
+  } else {
+    f.lo = *reinterpret_cast<const v4i*>(row + ((((MODE == F32 ? 2 : 4) * s + fq) ^ fsw) << 4));
+  }
+}
+
+// MFMAs of block rows [I0, I1) of fc, with the reads of fn (sub-step s of sa/sb; B fragments
+// first, then A rows in order, as the next sub-step consumes them) spread evenly over those
+// rows.  Scheduling fences keep each read ahead of the MFMA row it is placed before; left
+// alone, the compiler sinks every read next to its first use, which exposes the LDS latency.
+// Measured on the 16 x 16 modes: INT8 +1-4%, BF16 +2-4%; FP8 (two reads per fragment, 253
+// VGPRs) ran 0-4% slower this way and keeps the compiler's order.
+template <int MODE, class G, int I0, int I1>
+__device__ __forceinline__ void mfma_rows_reading(AccTile<MODE, G>& acc, const FragSet<MODE, G>& fc,
+                                                  FragSet<MODE, G>& fn, const uint8_t* sa, const uint8_t* sb,
+                                                  int s, int a_row0, int b_row0, int fq, int fsw) {
+  constexpr int FM = Blk<MODE, G>::FM, FN = Blk<MODE, G>::FN, MD = Blk<MODE, G>::MD;
+  constexpr int NR = FM + FN, ROWS = I1 - I0;
+#pragma unroll
+  for (int k = 0; k < ROWS; ++k) {
+#pragma unroll
+    for (int r = k * NR / ROWS; r < (k + 1) * NR / ROWS; ++r) {
+      if (r < FN) read_frag<MODE>(sb + (b_row0 + MD * r) * BKB, s, fq, fsw, fn.b[r]);
+      else read_frag<MODE>(sa + (a_row0 + MD * (r - FN)) * BKB, s, fq, fsw, fn.a[r - FN]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) mfma<MODE>(acc[I0 + k][j], fc.a[I0 + k], fc.b[j]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Number of 128-byte K stages of a row of Kb bytes.
 __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 1) / BKB; }
 
@@ -309,6 +347,7 @@ __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 
 //
 // Two stage buffers.  Per stage kt (buffer kt & 1, SUB sub-steps):
 //   read sub-step s+1 fragments | MFMAs of sub-step s            (s < SUB - 1)
+//   (16 x 16 modes: the reads are interleaved with the MFMA rows, see mfma_rows_reading)
 //   MFMAs of the last sub-step, first half of the block rows
 //   wait for own stage kt+1 loads and all LDS reads; barrier  (stage kt+1 visible, buffer free)
 //   DMA stage kt+2 into buffer kt & 1
@@ -319,12 +358,13 @@ __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 
 //
 // The loop covers the 128-byte K stages [kt_begin, kt_begin + kt_count); a split-K launch
 // gives each workgroup one such range (stages past the range, like chunks past K, load zeros).
-template <int MODE, class G>
+template <int MODE, class G, bool PIPELINED = Traits<MODE>::MD == 16>
 __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int M,
                                              int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc,
                                              int64_t kt_begin, int64_t kt_count) {
   constexpr int SUB = Traits<MODE>::sub_steps;
   static_assert(SUB % 2 == 0, "the last sub-step of a stage uses the second fragment set");
+  static_assert(!PIPELINED || Traits<MODE>::MD == 16, "interleaved reads are measured for 16 x 16 modes");
   constexpr int FM = Blk<MODE, G>::FM;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -373,8 +413,13 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
     constexpr int CUR = decltype(cur_tag)::value, NXT = CUR ^ 1;
 #pragma unroll
     for (int s = 0; s + 1 < SUB; ++s) {
-      read_frags<MODE, G>(stage_a<CUR>(), stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw, (s & 1) ? f0 : f1);
-      mfma_rows<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0);
+      if constexpr (PIPELINED) {
+        mfma_rows_reading<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0, (s & 1) ? f0 : f1, stage_a<CUR>(),
+                                          stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw);
+      } else {
+        read_frags<MODE, G>(stage_a<CUR>(), stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw, (s & 1) ? f0 : f1);
+        mfma_rows<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0);
+      }
     }
     mfma_rows<MODE, G, 0, FM / 2>(acc, f1);
     wait_stage<0>();
@@ -382,8 +427,13 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     stage_barrier();
     dma(stage_a<CUR>(), stage_b<CUR>(), kt + 2);
-    read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw, f0);
-    mfma_rows<MODE, G, FM / 2, FM>(acc, f1);
+    if constexpr (PIPELINED) {
+      mfma_rows_reading<MODE, G, FM / 2, FM>(acc, f1, f0, stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq,
+                                             fsw);
+    } else {
+      read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw, f0);
+      mfma_rows<MODE, G, FM / 2, FM>(acc, f1);
+    }
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
