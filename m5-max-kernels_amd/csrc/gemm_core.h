@@ -133,14 +133,14 @@ __device__ __forceinline__ void mfma(typename Traits<MODE>::acc_t& acc, const Fr
 // 8 XCDs (bid % 8); renumber so that each XCD receives a contiguous run of logical tiles,
 // then raster the logical order in bands of GROUP_M tile-rows (column-major inside a
 // band), so an XCD's concurrent tiles share A rows and B rows in its own L2.
-__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  int logical = bid;
-  if (total >= 16) {
-    const int per = total >> 3, rem = total & 7;
-    const int xcd = bid & 7, local = bid >> 3;
-    logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
-  }
+__device__ __forceinline__ int xcd_logical(int bid, int total) {
+  if (total < 16) return bid;
+  const int per = total >> 3, rem = total & 7;
+  const int xcd = bid & 7, local = bid >> 3;
+  return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
+}
+
+__device__ __forceinline__ void band_coords(int logical, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int band_size = GROUP_M * tiles_n;
   const int band = logical / band_size;
   const int first = band * GROUP_M;
@@ -148,6 +148,10 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   const int inner = logical - band * band_size;
   tm = first + inner % h;
   tn = inner / h;
+}
+
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  band_coords(xcd_logical(bid, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // LDS layout of one operand stage: 256 rows x 128 bytes (one L2 line per row); the 16-byte

@@ -33,19 +33,12 @@ struct EpiParams {
 // Wave grid used by every GEMM kernel of the library.
 using KernelGrid = Grid8;
 
-template <int MODE, bool ALIGNED, int OUT_DT, int BIAS, int GATE, bool RAW>
-__global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
-                                                                      const uint8_t* __restrict__ B, int M, int N,
-                                                                      int64_t Kb, EpiParams p) {
+// Scale epilogue of one 256 x 256 tile (every thread of the workgroup calls it; the LDS is
+// free).  RAW writes the INT32 accumulators.
+template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
+__device__ __forceinline__ void epilogue(const AccTile<MODE, KernelGrid>& acc, int M, int N, int m0, int n0,
+                                         const EpiParams& p) {
   using G = KernelGrid;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  AccTile<MODE, G> acc;
-  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
-  else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
-
   auto scaled = [&](int m, int n, auto v) {
     float value;
     if constexpr (MODE == I8 || MODE == F8) value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
@@ -120,6 +113,21 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint
       }
     }
   });
+}
+
+template <int MODE, bool ALIGNED, int OUT_DT, int BIAS, int GATE, bool RAW>
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
+                                                                      const uint8_t* __restrict__ B, int M, int N,
+                                                                      int64_t Kb, EpiParams p) {
+  using G = KernelGrid;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  AccTile<MODE, G> acc;
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+  else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+  epilogue<MODE, OUT_DT, BIAS, GATE, RAW>(acc, M, N, m0, n0, p);
 }
 
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>

@@ -100,6 +100,41 @@ def splitk_plan(m, n, k):
     return splits if splits >= 2 else 1
 
 
+def tail_split_plan(m, n, k, cus=256):
+    """Row split of a W8A8 linear with a partial last round: (rows, splits) or None.
+
+    With T tiles of 256 x 256 on `cus` CUs (one workgroup per CU, T >= cus), the last round
+    runs at (T mod cus) / cus of the chip.  The first `rows` rows (whole tile rows filling
+    at most the full rounds) then run as a plain launch and the remaining rows as a split-K
+    launch with `splits` K ranges per tile, which refills the last round.  The split saves
+    (1 - 1/splits) of a round and costs its INT32 partials, 8 * splits * (m - rows) * n
+    bytes written and read, plus a second launch.  Cost model from MI355X measurements: a
+    round of 256 x 256 tiles takes ~15.3 ns per unit of K (~2.2 POP/s), the partials move at
+    ~5 TB/s and a launch costs ~4 us; the split is taken when it saves over 5% of the plain
+    time.  (Measured: H3 widths N 5120-5376 at M 4096 7-18% faster; M 9914, N 4096, K 4096
+    no faster, and the model declines it.)"""
+    tiles_m, tiles_n = -(-m // 256), -(-n // 256)
+    tiles = tiles_m * tiles_n
+    if tiles < cus or tiles % cus == 0:
+        return None
+    rows_dp = (tiles // cus) * cus // tiles_n
+    tail_tiles = (tiles_m - rows_dp) * tiles_n
+    if rows_dp == 0:
+        return None
+    tail_m = m - rows_dp * 256
+    round_s = 15.3e-9 * k
+    best, best_gain = None, 0.05 * round_s * -(-tiles // cus)
+    for splits in range(2, min(cus // tail_tiles, -(-k // 128) // 2, 16) + 1):
+        gain = round_s * (1 - 1 / splits) - (tail_m * n * (8 * splits + 2) / 5e12 + 4e-6)
+        if gain > best_gain:
+            best, best_gain = splits, gain
+    return None if best is None else (rows_dp * 256, best)
+
+
+def _cu_count(device):
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
 def gemm(
     a,
     b,
@@ -214,7 +249,29 @@ def gemm(
         if bias is not None:
             bias = _lib.device_tensor(bias, "bias")
             bias_row_map = None if bias_row_map is None else _lib.device_tensor(bias_row_map, "bias_row_map")
-        splits = splitk_plan(m, n, k) if k % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 else 1
+        aligned = k % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
+        splits = splitk_plan(m, n, k) if aligned else 1
+        tail = tail_split_plan(m, n, k, _cu_count(a.device)) if aligned and splits == 1 else None
+        if tail is not None:
+            # Whole tile rows in full rounds, then the remaining rows split along K.  Every
+            # row-indexed operand is sliced at the same row; both launches are bit-exact.
+            r0, tail_splits = tail
+
+            def rows(t, lo, hi):
+                return None if t is None else t[lo:hi]
+
+            workspace = torch.empty((tail_splits, m - r0, n), dtype=torch.int32, device=a.device)
+            for lo, hi, part in ((0, r0, 1), (r0, m, tail_splits)):
+                args = [
+                    _lib.ptr(a[lo:hi]), _lib.ptr(b), hi - lo, n, k, _lib.ptr(a_scales[lo:hi]), _lib.ptr(b_scales),
+                    _lib.ptr(c[lo:hi]), out_code, _lib.ptr(bias), _lib.ptr(rows(bias_row_map, lo, hi)),
+                    _lib.ptr(rows(residual, lo, hi)), _lib.ptr(gate), _lib.ptr(rows(gate_row_map, lo, hi)),
+                ]
+                if part == 1:
+                    _lib.call("m5k_gemm_i8", *args, stream)
+                else:
+                    _lib.call("m5k_gemm_i8_splitk", *args, part, _lib.ptr(workspace), workspace.numel(), stream)
+            return c
         if splits > 1:
             workspace = torch.empty((splits, m, n), dtype=torch.int32, device=a.device)
             _lib.call(

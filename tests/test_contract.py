@@ -197,3 +197,28 @@ def test_shift_split_validation():
         shift_split_condition(g, g, g.float(), w, bias_backend="mpp-bf16-to-fp32")
     with pytest.raises(ValueError, match="ROCm device"):
         shift_split_condition(g, g, g, w)
+
+
+def test_tail_split_plan_decisions():
+    """Host schedule of the W8A8 linear on 256 CUs: the row split is taken where the measured
+    cost model says it pays (H3 widths at M 4096) and declined where it does not (M 9914 x
+    4096 x 4096, short K, tails over half a round, whole rounds, few-tile shapes)."""
+    from m5kernels_amd.hip import splitk_plan, tail_split_plan
+
+    assert tail_split_plan(4096, 5376, 5376) == (3072, 3)
+    assert tail_split_plan(4096, 5376, 14336) == (3072, 3)
+    assert tail_split_plan(4352, 4096, 2048) == (4096, 4)
+    for shape in [(9914, 4096, 4096), (4096, 5376, 2048), (4096, 14336, 5376), (4096, 7168, 5376),
+                  (4096, 4096, 16384), (1024, 5376, 5376)]:
+        assert tail_split_plan(*shape) is None, shape
+    assert splitk_plan(1024, 5376, 5376) == 2  # fewer tiles than CUs: the split-K schedule
+    for m in range(256, 12000, 397):
+        for n in (1536, 4096, 5120, 5376, 7168):
+            plan = tail_split_plan(m, n, 4096)
+            if plan is None:
+                continue
+            rows, splits = plan
+            tiles_n = -(-n // 256)
+            assert rows % 256 == 0 and 0 < rows < m and 2 <= splits <= 16
+            assert (rows // 256) * tiles_n <= ((-(-m // 256) * tiles_n) // 256) * 256
+            assert (-(-(m - rows) // 256)) * tiles_n * splits <= 256

@@ -318,3 +318,46 @@ def test_splitk_plan_and_routing(device):
         acc = ref.c_gemm_i8_acc(np_of(a), np_of(b))
         expected = ref.c_i8_epilogue(acc, np_of(sa), np_of(sb), out="bf16")
         np.testing.assert_array_equal(bits_of(y), expected)
+
+
+
+# Shapes with a partial last round that gemm() splits by rows (256 CUs): 336 tiles (tail rows
+# 1024, 3 K ranges), 272 tiles (tail rows 256, 4 ranges), 288 tiles with a ragged last tile
+# row (tail rows 304).
+_TAIL_CASES = [(4096, 5376, 5376), (4352, 4096, 2048), (4400, 4096, 2048)]
+
+
+@pytest.mark.parametrize("shape", _TAIL_CASES)
+@pytest.mark.parametrize("epilogue", ["bf16", "fp32", "fp16", "bias", "bias_table", "gate", "gate_table"])
+def test_tail_split_bit_identical_to_plain(shape, epilogue, device):
+    """gemm() runs whole tile rows as a plain launch and the rest as split-K, slicing every
+    row-indexed operand (scales, row maps, residual, output) at the same row; the result
+    matches one plain m5k_gemm_i8 launch bit for bit."""
+    from m5kernels_amd.hip import tail_split_plan
+
+    m, n, k = shape
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip("shapes chosen for 256 CUs")
+    assert tail_split_plan(m, n, k, cus) is not None
+    g = torch.Generator(device="cpu").manual_seed(m + n + k)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
+    sa = (torch.rand(m, generator=g) * 0.01 + 1e-3).to(device)
+    sb = (torch.rand(n, generator=g) * 0.01 + 1e-3).to(device)
+    out = {"fp32": torch.float32, "fp16": torch.float16}.get(epilogue, torch.bfloat16)
+    rows = torch.tensor([(7 * i) % 3 for i in range(m)], dtype=torch.int32, device=device)
+    kw, call_kw = {}, {}
+    if epilogue.startswith("bias"):
+        kw["bias"] = torch.randn((3, n) if epilogue == "bias_table" else (n,), generator=g).to(device)
+        kw["bias_map"] = rows if epilogue == "bias_table" else None
+        call_kw = {"bias": kw["bias"], "bias_row_map": kw["bias_map"]}
+    elif epilogue.startswith("gate"):
+        kw["residual"] = torch.randn((m, n), generator=g).to(torch.bfloat16).to(device)
+        kw["gate"] = torch.randn((3, n) if epilogue == "gate_table" else (n,), generator=g).to(torch.bfloat16).to(device)
+        kw["gate_map"] = rows if epilogue == "gate_table" else None
+        call_kw = {"residual": kw["residual"], "gate": kw["gate"], "gate_row_map": kw["gate_map"]}
+    plain = _gemm_i8_call("m5k_gemm_i8", a, b, sa, sb, out, **kw)
+    y = gemm(a, b, "int8", a_scales=sa, b_scales=sb, output_dtype=out, **call_kw)
+    view = torch.int16 if out != torch.float32 else torch.int32
+    assert torch.equal(plain.view(view), y.view(view))
