@@ -59,7 +59,6 @@ struct Grid {
   static constexpr int WAVES = WAVES_M * WAVES_N;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  static constexpr int FM = WM / 32, FN = WN / 32;
   static constexpr int DMA_ROWS = BM / WAVES;     // rows of each operand one wave DMAs per stage
   static constexpr int DMA_INSTR = DMA_ROWS / 8;  // 1 KiB (8 rows of 128 B) per instruction
 };
@@ -160,11 +159,17 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 // logical chunk, which lands on 16 distinct (row parity, physical chunk) bank groups.
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
-// All LDS of a GEMM kernel: NST stages x (A, B) x 32 KiB = 128 KiB.  The main loop uses it as
-// the stage ring; epilogues may reuse it afterwards (e.g. as a 256 x 256 BF16 tile).  The DMA
-// writes are inline asm with "memory" clobbers and every consumer sits behind an explicit
-// wait and barrier, so one array serves all stages.
-constexpr int LDS_BYTES = NST * 2 * STAGE_BYTES;
+// Row stride (elements) of a 256 x 256 16-bit tile staged in LDS by an epilogue: 528 bytes, so
+// the four rows a wave writes per accumulator register (rows 4 apart) land 16 banks apart
+// instead of on the same 8 banks, and 16-byte row chunks stay aligned.
+constexpr int TILE16_STRIDE = BN + 8;
+
+// All LDS of a GEMM kernel: NST stages x (A, B) x 32 KiB = 128 KiB for the main loop, which uses
+// it as the stage ring; epilogues may reuse it afterwards (a 256 x TILE16_STRIDE 16-bit tile,
+// 132 KiB).  The DMA writes are inline asm with "memory" clobbers and every consumer sits
+// behind an explicit wait and barrier, so one array serves all stages.
+constexpr int LDS_BYTES = NST * 2 * STAGE_BYTES > BM * TILE16_STRIDE * 2 ? NST * 2 * STAGE_BYTES
+                                                                         : BM * TILE16_STRIDE * 2;
 __shared__ __attribute__((aligned(16))) uint8_t g_lds[LDS_BYTES];
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;

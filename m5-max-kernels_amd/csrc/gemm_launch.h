@@ -57,7 +57,7 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, KernelGrid>& acc, i
       uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
       for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
         const float value = (m < M && n < N) ? scaled(m, n, v) : 0.0f;
-        tile[(m - m0) * BN + (n - n0)] = static_cast<uint16_t>(
+        tile[(m - m0) * TILE16_STRIDE + (n - n0)] = static_cast<uint16_t>(
             GATE != EPI_NONE || OUT_DT == M5K_BF16 ? f32_to_bf16_bits(value) : f32_to_f16_bits(value));
       });
       __syncthreads();
@@ -65,7 +65,7 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, KernelGrid>& acc, i
         const int r = c >> 5, cc = c & 31;
         const int m = m0 + r, n = n0 + 8 * cc;
         if (m >= M || n >= N) continue;  // N % 8 == 0: a chunk is wholly in or out
-        uint4 w = *reinterpret_cast<const uint4*>(tile + r * BN + 8 * cc);
+        uint4 w = *reinterpret_cast<const uint4*>(tile + r * TILE16_STRIDE + 8 * cc);
         const int64_t idx = (int64_t)m * N + n;
         if constexpr (GATE != EPI_NONE) {
           const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;

@@ -147,16 +147,28 @@ __device__ __forceinline__ void unpack8_bf16(const uint4& w, float (&v)[8]) {
   }
 }
 
+// Sum over each 16-lane row, the same pairings as xor butterflies 1, 2, 4, 8: quad_perm
+// [1,0,3,2] and [2,3,0,1] are xor 1 and 2; after them every lane of a quad holds the same bits,
+// so row_half_mirror (lane i <- 7 - i) adds the same quad as xor 4 and row_mirror (lane
+// i <- 15 - i) the same half-row as xor 8.  The sums commute, so all 16 lanes end with the
+// bits the xor butterflies give.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_move<0xB1>(v);
+  v += dpp_move<0x4E>(v);
+  v += dpp_move<0x141>(v);
+  v += dpp_move<0x140>(v);
+  return v;
+}
+
 // Normalize + rotate one (row, head) held as z[8] per lane; returns the packed BF16 output.
+// HALF8: rope_half == 64, every partner lane is lg ^ 8 (one row_ror:8 DPP move).
+template <bool HALF8>
 __device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneRope& r, const uint4& cw,
                                                 const uint4& sw, float eps) {
   float ss = 0.0f;
 #pragma unroll
   for (int t = 0; t < 8; ++t) ss += z[t] * z[t];
-  ss += __shfl_xor(ss, 1, 16);
-  ss += __shfl_xor(ss, 2, 16);
-  ss += __shfl_xor(ss, 4, 16);
-  ss += __shfl_xor(ss, 8, 16);
+  ss = row16_sum(ss);
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(HEAD) + eps);
   float u[8], c[8], s[8];
   unpack8_bf16(cw, c);
@@ -169,7 +181,7 @@ __device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneR
     float y[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const float pu = __shfl(u[t + e], r.src, 16);
+      const float pu = HALF8 ? dpp_move<0x128>(u[t + e]) : __shfl(u[t + e], r.src, 16);
       const float a = u[t + e] * c[t + e], b = pu * s[t + e];
       y[e] = !r.rot ? u[t + e] : r.lower ? a - b : a + b;
     }
@@ -213,14 +225,14 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
     }
   }
 
-  // BF16 projection tile [256 rows][256 cols] in LDS (row stride 512 B).  The main loop ended
-  // with a drained DMA and a barrier, so the stage ring is free.
+  // BF16 projection tile [256 rows][256 cols] in LDS (row stride TILE16_STRIDE).  The main
+  // loop ended with a drained DMA and a barrier, so the stage ring is free.
   uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
   for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
     float value;
     if constexpr (MODE == I8) value = (m < M && n < N) ? (static_cast<float>(v) * sa[m]) * sb[n] : 0.0f;
     else value = v;
-    tile[(m - m0) * BN + (n - n0)] = static_cast<uint16_t>(f32_to_bf16_bits(value));
+    tile[(m - m0) * TILE16_STRIDE + (n - n0)] = static_cast<uint16_t>(f32_to_bf16_bits(value));
   });
   __syncthreads();
 
@@ -233,7 +245,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         if (h >= heads_here) continue;
-        const uint16_t* src = tile + local_row * BN + h * HEAD;
+        const uint16_t* src = tile + local_row * TILE16_STRIDE + h * HEAD;
         const BlockDst d = block_dst(p, n0 / HEAD + h);  // uniform across the group
         const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
         uint4* dst = reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg);
@@ -243,7 +255,9 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
         }
         float z[8];
         unpack8_bf16(w, z);
-        *dst = norm_rope_fast(z, d.gamma == p.gamma ? lr : lrk, cw[i], sw[i], p.eps);
+        const LaneRope& rr = d.gamma == p.gamma ? lr : lrk;
+        *dst = p.rope_half == 64 ? norm_rope_fast<true>(z, rr, cw[i], sw[i], p.eps)
+                                 : norm_rope_fast<false>(z, rr, cw[i], sw[i], p.eps);
       }
     }
     return;
@@ -253,7 +267,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
     const int row = m0 + local_row;
     const int block = n0 / HEAD + local_head;
     if (row >= M || block * HEAD >= N) continue;  // uniform across the 16-lane group
-    const uint16_t* src = tile + local_row * BN + local_head * HEAD;
+    const uint16_t* src = tile + local_row * TILE16_STRIDE + local_head * HEAD;
     const BlockDst d = block_dst(p, block);
     if (d.gamma == nullptr) {
       *reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg) =
@@ -286,7 +300,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
     const LaneRope lr = lane_rope(p, p.gamma, lg);
     uint4 cw, sw;
     lane_cos_sin(p, lr, row, lg, cw, sw);
-    const uint4 out = norm_rope_fast(z, lr, cw, sw, p.eps);
+    const uint4 out = p.rope_half == 64 ? norm_rope_fast<true>(z, lr, cw, sw, p.eps)
+                                        : norm_rope_fast<false>(z, lr, cw, sw, p.eps);
     *reinterpret_cast<uint4*>(p.y + (static_cast<int64_t>(head) * M + row) * HEAD + 8 * lg) = out;
     return;
   }
