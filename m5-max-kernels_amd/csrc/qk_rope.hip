@@ -202,28 +202,18 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   AccTile<MODE, G> acc;
-  // The compiler's read order: with interleaved reads this kernel's epilogue state spills
-  // inside the main loop, which measured 3-8% slower at M 9914.
-  if constexpr (ALIGNED) mainloop_dma<MODE, G, false>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
 
-  const int group = threadIdx.x >> 4, lg = threadIdx.x & 15;
+  // Everything the epilogue loads depends on the lane index taken here, after the main loop,
+  // so no epilogue value is hoisted into the loop's register budget (with the interleaved
+  // fragment reads the loop uses 241 of 256 VGPRs).
+  int tid_after = threadIdx.x;
+  __asm__ volatile("" : "+v"(tid_after));
+  const int group = tid_after >> 4, lg = tid_after & 15;
   constexpr int GROUPS = G::THREADS / 16;  // 32 groups of 16 lanes
   constexpr int ROWS_PER_GROUP = BM / GROUPS;
   const int heads_here = (N - n0) >= BN ? 2 : 1;  // N is a multiple of 128
-
-  // Fast path: issue the per-row cos/sin loads of this group's rows before staging the tile.
-  LaneRope lr, lrk;  // Q (or single-projection) gamma; K gamma in the grouped layout
-  uint4 cw[ROWS_PER_GROUP], sw[ROWS_PER_GROUP];
-  if (fast) {
-    lr = lane_rope(p, p.gamma, lg);
-    if (p.grouped) lrk = lane_rope(p, p.k_gamma, lg);
-#pragma unroll
-    for (int i = 0; i < ROWS_PER_GROUP; ++i) {
-      const int row = m0 + group + GROUPS * i;
-      if (row < M) lane_cos_sin(p, lr, row, lg, cw[i], sw[i]);
-    }
-  }
 
   // BF16 projection tile [256 rows][256 cols] in LDS (row stride TILE16_STRIDE).  The main
   // loop ended with a drained DMA and a barrier, so the stage ring is free.
@@ -234,6 +224,22 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
     else value = v;
     tile[(m - m0) * TILE16_STRIDE + (n - n0)] = static_cast<uint16_t>(f32_to_bf16_bits(value));
   });
+  // Fast path: issue the per-row cos/sin loads of this group's rows once the accumulators are
+  // staged (their 64 registers are free then); the barrier below covers their latency.
+  LaneRope lr, lrk;  // Q (or single-projection) gamma; K gamma in the grouped layout
+  uint4 cw[ROWS_PER_GROUP], sw[ROWS_PER_GROUP];
+  int row0 = m0 + group;
+  __asm__ volatile("" : "+v"(row0));
+  if (fast) {
+    lr = lane_rope(p, p.gamma, lg);
+    if (p.grouped) lrk = lane_rope(p, p.k_gamma, lg);
+#pragma unroll
+    for (int i = 0; i < ROWS_PER_GROUP; ++i) {
+      const int row = row0 + GROUPS * i;
+      if (row < M) lane_cos_sin(p, lr, row, lg, cw[i], sw[i]);
+    }
+  }
+
   __syncthreads();
 
   if (fast) {
