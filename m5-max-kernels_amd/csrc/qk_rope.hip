@@ -13,7 +13,7 @@
 // contraction).
 //
 // The fused kernel runs the GEMM main loop for a 256-row x 2-head tile, stages the BF16
-// projection in the (then free) 128 KiB of LDS, and normalizes each (row, head) with a group
+// projection in the (then free) LDS, and normalizes each (row, head) with a group
 // of 16 lanes (8 channels each, one 16-byte read and one 16-byte head-major store per lane).
 // The staged kernel runs the same per-(row, head) routine on a BF16 [M,N] projection in HBM,
 // so the two paths agree bit for bit whenever their projections do.
