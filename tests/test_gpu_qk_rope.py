@@ -62,12 +62,15 @@ def _projection(a, b, mode, sa=None, sb=None):
         ((7, 128, 16), (16, 128, 8, 1)),
     ],
 )
-def test_fused_projection_tiles_tails_and_reference(mode, shape, tile, device):
+@pytest.mark.parametrize("rope_half", [48, 64])
+def test_fused_projection_tiles_tails_and_reference(mode, shape, tile, rope_half, device):
+    """Fused and staged Q/K equal bitwise and match the reference; R = 64 takes the DPP
+    partner exchange (lane lg ^ 8), R = 48 the general shuffle."""
     rng = np.random.default_rng(117)
     m, n, k = shape
     a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(torch.bfloat16)
     b = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device).to(torch.bfloat16)
-    gamma, cos, sin = _tables(rng, m, device)
+    gamma, cos, sin = _tables(rng, m, device, rope_half)
     scales = {}
     if mode == "int8":
         a, sa = quantize(a, "int8")
