@@ -10,9 +10,10 @@
 //
 // A row is read once from HBM with 16-byte loads and held in VGPRs between the max
 // reduction and the encode, so HBM traffic is exactly 2*K (bf16 in) + K (codes out) + 4
-// bytes per row.  Each row has its own workgroup of 4 wave64.  With the encode at about
-// eight VALU ops per element the kernel runs within ~15% of a plain copy of the same bytes;
-// a persistent grid with a one-row register prefetch measured no faster.
+// bytes per row.  Each row has its own workgroup of 4 wave64.  At [4096, 16384] the kernel
+// takes 37 us where the same traffic with no arithmetic streams in 26 us: the encode's ~7
+// VALU ops per element are the difference.  A persistent grid with a one-row register
+// prefetch, and a variant at 8 waves per SIMD, measured no faster.
 #include "m5k_common.h"
 
 namespace m5k {
