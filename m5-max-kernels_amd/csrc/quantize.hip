@@ -86,16 +86,8 @@ __device__ __forceinline__ void encode_chunk(const uint4& v, const I8Scale& s, u
     }
   }
   uint32_t packed[EPC / 4];
-  if constexpr (MODE == M5K_QUANT_INT8) {
-    encode_i8<EPC>(f, s, packed);
-  } else {
-#pragma unroll
-    for (int j = 0; j < EPC / 4; ++j) {
-      packed[j] = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) packed[j] |= fp8_e4m3_encode(f[4 * j + b] / s.scale) << (8 * b);
-    }
-  }
+  if constexpr (MODE == M5K_QUANT_INT8) encode_i8<EPC>(f, s, packed);
+  else encode_fp8<EPC>(f, s, packed);
   if constexpr (EPC == 8) *reinterpret_cast<uint2*>(out) = make_uint2(packed[0], packed[1]);
   else *reinterpret_cast<uint32_t*>(out) = packed[0];
 }

@@ -160,6 +160,29 @@ def test_fp8_ties_and_saturation(device):
     np.testing.assert_array_equal(np_of(q)[0], ref.fp8_encode(row))
 
 
+@pytest.mark.parametrize("m", [7, 4095])
+def test_fp8_dense_ties_bit_exact(m, device):
+    """Rows with peak 448 m make the scale exactly m, so x = m * (midpoint of two adjacent E4M3
+    values) is an exact tie of x / scale.  The reciprocal product misses some ties, so the
+    encoder's bracket check must send those groups to the IEEE division; neighbours one ulp
+    either side check the rounding just off each boundary, and -x the sign."""
+    table = ref.fp8_decode(np.arange(127, dtype=np.uint8)).astype(np.float64)
+    mids = ((table[:-1] + table[1:]) / 2) * m
+    ties = mids.astype(np.float32)
+    assert np.all(ties.astype(np.float64) == mids)  # exact in float32
+    row = np.concatenate([[448.0 * m], ties, np.nextafter(ties, np.float32(np.inf)),
+                          np.nextafter(ties, np.float32(0))]).astype(np.float32)
+    row = np.resize(row, 2048)
+    x = np.stack([row, -row, np.roll(row, 3)])
+    q, s = quantize(torch.from_numpy(x).to(device), "fp8")
+    rq, rs = ref.c_quantize_rows(x, "fp8")
+    assert np.all(rs == np.float32(m))
+    fast = ref.fp8_encode((x * (np.float32(1) / np.float32(m))).astype(np.float32))
+    assert np.count_nonzero(fast != rq) > 0  # the reciprocal alone would fail these rows
+    np.testing.assert_array_equal(np_of(s), rs)
+    np.testing.assert_array_equal(np_of(q), rq)
+
+
 def test_inputs_not_mutated_and_strided(device):
     base = torch.randn(64, 512, device=device, dtype=torch.bfloat16)
     view = base[:, ::2]
