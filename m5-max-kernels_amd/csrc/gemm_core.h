@@ -53,17 +53,23 @@ constexpr int GROUP_M = 4;             // tile-rows per raster band
 // (256/WAVES_N) sub-tile of MFMA blocks.  2 x 2 = one wave per SIMD with 256 accumulator
 // registers; 2 x 4 = two waves per SIMD with 128 each, so one wave's MFMAs keep the pipe busy
 // while its sibling waits at a barrier.
-template <int WAVES_M_, int WAVES_N_>
+// TN is the tile's column count: BN for the full tile, BN / 2 for the half-width tiles that
+// refill a partial last round.
+template <int WAVES_M_, int WAVES_N_, int TN_ = BN>
 struct Grid {
   static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
   static constexpr int WAVES = WAVES_M * WAVES_N;
   static constexpr int THREADS = 64 * WAVES;
-  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  static constexpr int DMA_ROWS = BM / WAVES;     // rows of each operand one wave DMAs per stage
-  static constexpr int DMA_INSTR = DMA_ROWS / 8;  // 1 KiB (8 rows of 128 B) per instruction
+  static constexpr int TN = TN_;
+  static constexpr int WM = BM / WAVES_M, WN = TN / WAVES_N;
+  static constexpr int DMA_ROWS = BM / WAVES;       // A rows one wave DMAs per stage
+  static constexpr int DMA_INSTR = DMA_ROWS / 8;    // 1 KiB (8 rows of 128 B) per instruction
+  static constexpr int DMA_ROWS_B = TN / WAVES;     // B rows one wave DMAs per stage
+  static constexpr int DMA_INSTR_B = DMA_ROWS_B / 8;
 };
 using Grid4 = Grid<2, 2>;
 using Grid8 = Grid<2, 4>;
+using Grid8Half = Grid<4, 2, BN / 2>;  // 256 x 128 tile, 8 waves of 64 x 64
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <int MODE>
@@ -389,26 +395,32 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   // offset of the logical chunk the lane moves.  Instruction i covers rows
   // wave * DMA_ROWS + 8i + [0, 8) (DMA_ROWS a multiple of 16), whose swizzle is
   // 4 (i & 1) + (l >> 4): the chunk offset depends on the parity of i only.
-  static_assert(G::DMA_ROWS % 16 == 0, "DMA row groups start at even row pairs");
+  static_assert(G::DMA_ROWS % 16 == 0 && G::DMA_ROWS_B % 16 == 0, "DMA row groups start at even row pairs");
   const uint32_t lchunk[2] = {static_cast<uint32_t>(((lane & 7) ^ (lane >> 4)) << 4),
                               static_cast<uint32_t>(((lane & 7) ^ (4 + (lane >> 4))) << 4)};
-  uint32_t a_base[G::DMA_INSTR], b_base[G::DMA_INSTR];
+  uint32_t a_base[G::DMA_INSTR], b_base[G::DMA_INSTR_B];
 #pragma unroll
   for (int i = 0; i < G::DMA_INSTR; ++i) {
     const int r = wave * G::DMA_ROWS + 8 * i + (lane >> 3);
     a_base[i] = tile_m0 + r < M ? static_cast<uint32_t>((int64_t)(tile_m0 + r) * Kb) + lchunk[i & 1] : kOob;
+  }
+#pragma unroll
+  for (int i = 0; i < G::DMA_INSTR_B; ++i) {
+    const int r = wave * G::DMA_ROWS_B + 8 * i + (lane >> 3);
     b_base[i] = tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb) + lchunk[i & 1] : kOob;
   }
   const uint32_t lds_row0 = static_cast<uint32_t>(uwave * G::DMA_ROWS * BKB);
+  const uint32_t lds_row0_b = static_cast<uint32_t>(uwave * G::DMA_ROWS_B * BKB);
   auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {  // kr: stage index relative to kt_begin
     const uint32_t kofs = static_cast<uint32_t>((kt_begin + kr) * BKB);
     const bool live = kr < kt_count;
-    const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0;
+    const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0_b;
 #pragma unroll
     for (int i = 0; i < G::DMA_INSTR; ++i) {
       const bool kin = live && static_cast<int64_t>(kofs) + lchunk[i & 1] < Kb;
       dma16(la + 8 * i * BKB, (kin && a_base[i] != kOob) ? a_base[i] + kofs : kOob, rsrc_a);
-      dma16(lb + 8 * i * BKB, (kin && b_base[i] != kOob) ? b_base[i] + kofs : kOob, rsrc_b);
+      if (i < G::DMA_INSTR_B)
+        dma16(lb + 8 * i * BKB, (kin && b_base[i] != kOob) ? b_base[i] + kofs : kOob, rsrc_b);
     }
   };
 
@@ -449,7 +461,7 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
 
   dma(stage_a<0>(), stage_b<0>(), 0);
   dma(stage_a<1>(), stage_b<1>(), 1);
-  wait_stage<2 * G::DMA_INSTR>();  // stage 0 landed (own loads)
+  wait_stage<G::DMA_INSTR + G::DMA_INSTR_B>();  // stage 0 landed (own loads)
   stage_barrier();
   read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fq, fsw, f0);
   const int64_t kt_padded = (kt_count + 1) / 2 * 2;
@@ -483,7 +495,7 @@ __device__ __forceinline__ void mainloop_staged(const uint8_t* __restrict__ A, c
     const int64_t kb = kt * BKB + lc * 16;
     for (int i = 0; i < BM / ROWS_PER_PASS; ++i) {
       const int r = lr + ROWS_PER_PASS * i;
-      const int am = tile_m0 + r, bn = tile_n0 + r;
+      const int am = tile_m0 + r, bn = r < G::TN ? tile_n0 + r : N;  // rows past the tile width: zeros
       uint32_t wa[4] = {0, 0, 0, 0}, wb[4] = {0, 0, 0, 0};
       for (int e = 0; e < 16; ++e) {
         const bool kin = kb + e < Kb;

@@ -9,6 +9,9 @@
 // The library is compiled with -ffp-contract=off so none of these products and sums is
 // fused into an FMA: the FP32 rounding sequence is exactly the one written above.
 #pragma once
+#include <algorithm>
+#include <cstdlib>
+
 #include "gemm_core.h"
 
 namespace m5k {
@@ -33,12 +36,11 @@ struct EpiParams {
 // Wave grid used by every GEMM kernel of the library.
 using KernelGrid = Grid8;
 
-// Scale epilogue of one 256 x 256 tile (every thread of the workgroup calls it; the LDS is
+// Scale epilogue of one 256 x G::TN tile (every thread of the workgroup calls it; the LDS is
 // free).  RAW writes the INT32 accumulators.
-template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
-__device__ __forceinline__ void epilogue(const AccTile<MODE, KernelGrid>& acc, int M, int N, int m0, int n0,
+template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW, class G = KernelGrid>
+__device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int N, int m0, int n0,
                                          const EpiParams& p) {
-  using G = KernelGrid;
   auto scaled = [&](int m, int n, auto v) {
     float value;
     if constexpr (MODE == I8 || MODE == F8) value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
@@ -61,8 +63,9 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, KernelGrid>& acc, i
             GATE != EPI_NONE || OUT_DT == M5K_BF16 ? f32_to_bf16_bits(value) : f32_to_f16_bits(value));
       });
       __syncthreads();
-      for (int c = threadIdx.x; c < BM * BN / 8; c += G::THREADS) {
-        const int r = c >> 5, cc = c & 31;
+      constexpr int CPR = G::TN / 8;  // 16-byte chunks per tile row
+      for (int c = threadIdx.x; c < BM * CPR; c += G::THREADS) {
+        const int r = c / CPR, cc = c % CPR;
         const int m = m0 + r, n = n0 + 8 * cc;
         if (m >= M || n >= N) continue;  // N % 8 == 0: a chunk is wholly in or out
         uint4 w = *reinterpret_cast<const uint4*>(tile + r * TILE16_STRIDE + 8 * cc);
@@ -130,6 +133,122 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint
   epilogue<MODE, OUT_DT, BIAS, GATE, RAW>(acc, M, N, m0, n0, p);
 }
 
+// ---- Mixed tiles for a partial last round ---------------------------------------------------
+//
+// T tiles on C CUs (one workgroup per CU) take ceil(T / C) rounds; when the last round is only
+// partly filled, most CUs idle through it.  The mixed launch keeps the leading tile rows as
+// 256 x 256 tiles and runs the last `tail` tile rows as 256 x 128 tiles, which take a little
+// over half as long, so the last round is shorter and better filled.  Each output element is
+// still one workgroup's dot product over all of K: results are bit-identical to the plain
+// launch.  Workgroups [0, full) are the 256 x 256 tiles of rows [0, rows_full); the 256 x 128
+// tiles of rows [rows_full, M) start at `full` rounded up to a multiple of 8, so both parts keep
+// the XCD-contiguous numbering of tile_coords (the workgroups in between exit at once).
+using HalfGrid = Grid8Half;
+
+template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_mixed_kernel(const uint8_t* __restrict__ A,
+                                                                            const uint8_t* __restrict__ B, int M,
+                                                                            int N, int64_t Kb, int rows_full,
+                                                                            EpiParams p) {
+  const int tiles_n = (N + BN - 1) / BN;
+  const int full = rows_full / BM * tiles_n;
+  const int half0 = (full + 7) & ~7;
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < full) {
+    using G = KernelGrid;
+    int tm, tn;
+    tile_coords(bid, rows_full / BM, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    AccTile<MODE, G> acc;
+    mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+    epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
+  } else if (bid >= half0) {
+    using G = HalfGrid;
+    int tm, tn;
+    tile_coords(bid - half0, (M - rows_full + BM - 1) / BM, (N + G::TN - 1) / G::TN, tm, tn);
+    const int m0 = rows_full + tm * BM, n0 = tn * G::TN;
+    AccTile<MODE, G> acc;
+    mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+    epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
+  }
+}
+
+constexpr int XCDS = 8;
+// Time of a 256 x 128 tile in units of a 256 x 256 tile's.
+constexpr double kHalfTileCost = 0.56;
+
+// Finish time, in 256 x 256 tile times, of one XCD running nf full tiles and then nh half
+// tiles on c CUs, each workgroup taken in order by the first free CU.
+inline double xcd_makespan(int64_t nf, int64_t nh, int c, double h) {
+  const int64_t F = nf / c, L = nf % c;  // L CUs run one more full tile than the other c - L
+  double end = L ? F + 1.0 : static_cast<double>(F);
+  if (nh == 0) return end;
+  // Half-tile slots open at F + i h on c - L CUs and at F + 1 + j h on L CUs; the jobs take the
+  // earliest nh of them.
+  int64_t i = 0, j = 0, left = nh;
+  double last = 0.0;
+  while (left > 0) {
+    const double t1 = F + i * h, t2 = F + 1.0 + j * h;
+    if (c - L > 0 && (L == 0 || t1 <= t2)) {
+      left -= c - L < left ? c - L : left;
+      last = t1;
+      ++i;
+    } else {
+      left -= L < left ? L : left;
+      last = t2;
+      ++j;
+    }
+  }
+  return end > last + h ? end : last + h;
+}
+
+inline double mixed_makespan(int64_t full, int64_t half, int cus) {
+  const int c = cus / XCDS;
+  double worst = 0.0;
+  for (int x = 0; x < XCDS; ++x) {
+    const int64_t nf = full / XCDS + (x < full % XCDS), nh = half / XCDS + (x < half % XCDS);
+    const double t = xcd_makespan(nf, nh, c, kHalfTileCost);
+    worst = t > worst ? t : worst;
+  }
+  return worst;
+}
+
+// Tile rows to run as 256 x 128 tiles (0: the plain launch), chosen by the makespan model
+// above and used only for a predicted gain of 5% or more.  The full-tile part must fill whole
+// rounds (or be empty), so the half tiles start together once every full tile is done:
+// measured on MI355X, half tiles that overlap a partial round of full tiles ran slower than
+// the model (N = 6144 at 1.5 rounds and N = 14336 at 3.5 rounds lost 4-8% against the plain
+// launch), while the whole-round splits matched or beat it (M = 9914, 4352, 2048, 1024).
+// M5K_GEMM_MIXED_TILES=0 in the environment turns the mixed launch off (read on every call).
+inline int64_t mixed_tail_rows(int64_t m, int64_t n, int cus) {
+  if (cus < XCDS) return 0;
+  if (const char* env = std::getenv("M5K_GEMM_MIXED_TILES"); env && env[0] == '0') return 0;
+  const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+  const int64_t tiles_nh = (n + HalfGrid::TN - 1) / HalfGrid::TN;
+  if (tiles_m * tiles_n > 64 * static_cast<int64_t>(cus)) return 0;  // a partial round is noise
+  struct Entry {
+    int64_t m_tiles, n, cus, rows;
+  };
+  static thread_local Entry memo[16] = {};
+  Entry& e = memo[(tiles_m * 31 + n * 7 + cus) & 15];
+  if (e.m_tiles == tiles_m && e.n == n && e.cus == cus) return e.rows;
+  const double plain = mixed_makespan(tiles_m * tiles_n, 0, cus);
+  // Only the rows of about one round are worth converting.
+  const int64_t max_rows = std::min<int64_t>(tiles_m, (cus + tiles_n - 1) / tiles_n + 1);
+  double best = plain * 0.95;
+  int64_t rows = 0;
+  for (int64_t r = 1; r <= max_rows; ++r) {
+    if ((tiles_m - r) * tiles_n % cus != 0) continue;
+    const double t = mixed_makespan((tiles_m - r) * tiles_n, r * tiles_nh, cus);
+    if (t < best) {
+      best = t;
+      rows = r;
+    }
+  }
+  e = Entry{tiles_m, n, cus, rows};
+  return rows;
+}
+
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
 int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
            hipStream_t st, const char* name) {
@@ -144,9 +263,17 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   auto* B = static_cast<const uint8_t*>(b);
   EpiParams q = p;
   q.coalesced = n % 8 == 0 && aligned16(p.c) && (p.residual == nullptr || (aligned16(p.residual) && aligned16(p.gate)));
-  if (aligned)
-    gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
-  else
+  if (aligned) {
+    if (const int64_t tail = mixed_tail_rows(m, n, device_cus())) {
+      const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
+      const int64_t full = (tiles_m - tail) * tiles_n;
+      const int64_t wgs = (full + 7) / 8 * 8 + tail * ((n + HalfGrid::TN - 1) / HalfGrid::TN);
+      gemm_mixed_kernel<MODE, OUT_DT, BIAS, GATE, RAW><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(
+          A, B, (int)m, (int)n, kb, static_cast<int>((tiles_m - tail) * BM), q);
+    } else {
+      gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
+    }
+  } else
     gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
   return launch_status(name);
 }

@@ -14,6 +14,8 @@ void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 // Translate a launch's hipGetLastError() into the ABI status.
 int launch_status(const char* what);
+// Compute units of the current device (cached per device; 0 if the query fails).
+int device_cus();
 
 #define M5K_REQUIRE(cond, ...)          \
   do {                                  \

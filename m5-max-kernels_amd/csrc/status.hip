@@ -1,6 +1,7 @@
 // Thread-local error message and launch-status helpers for the C ABI.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
@@ -26,6 +27,19 @@ int launch_status(const char* what) {
     return M5K_ELAUNCH;
   }
   return M5K_OK;
+}
+
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64) {
+    if (const int v = cache[dev].load(std::memory_order_relaxed)) return v;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
 }
 
 }  // namespace m5k

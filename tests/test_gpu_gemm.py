@@ -30,8 +30,19 @@ def _codes(m, n, k, seed=83, bound=127):
     return a, b, sa, sb
 
 
+@pytest.fixture(params=["auto", "plain"])
+def schedule(request, monkeypatch):
+    """Run a test under the library's launch choice ("auto": shapes with a partial last round
+    take the mixed 256 x 256 / 256 x 128 launch) and with that launch switched off."""
+    if request.param == "plain":
+        monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
+    else:
+        monkeypatch.delenv("M5K_GEMM_MIXED_TILES", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("shape", SHAPES)
-def test_int32_accumulators_bit_exact(shape, device):
+def test_int32_accumulators_bit_exact(shape, schedule, device):
     m, n, k = shape
     a, b, _, _ = _codes(m, n, k)
     acc = gemm_i8_accumulators(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
@@ -50,7 +61,7 @@ def test_int32_accumulators_worst_case_magnitude(device):
 
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("out", ["bf16", "fp32"])
-def test_w8a8_epilogue_bit_exact(shape, out, device):
+def test_w8a8_epilogue_bit_exact(shape, out, schedule, device):
     m, n, k = shape
     a, b, sa, sb = _codes(m, n, k)
     dt = torch.bfloat16 if out == "bf16" else torch.float32
@@ -161,7 +172,7 @@ def test_gated_epilogue(mode, mapped, device):
 
 
 @pytest.mark.parametrize("shape", [(1, 33, 128), (127, 65, 256), (300, 520, 1024), (256, 1024, 1024)])
-def test_fp8_gemm(shape, device):
+def test_fp8_gemm(shape, schedule, device):
     m, n, k = shape
     rng = np.random.default_rng(5)
     a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(torch.bfloat16)
@@ -192,7 +203,7 @@ def test_fp8_ones_kat(kats, device):
 
 @pytest.mark.parametrize("mode", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("shape", [(1, 33, 64), (127, 65, 96), (65, 17, 257), (300, 520, 1024), (257, 129, 4099)])
-def test_float_gemm(mode, shape, device):
+def test_float_gemm(mode, shape, schedule, device):
     """Float GEMMs with FP32 accumulation against a float64 product of the same operands.
     Output gates: the reference's implementation rel-L2 (bf16 0.008, fp16 1e-3, fp32 1e-4,
     engine.py gates) on the declared output dtype; FP32 output held to 1e-5 (FP32 accumulation
@@ -361,3 +372,69 @@ def test_tail_split_bit_identical_to_plain(shape, epilogue, device):
     y = gemm(a, b, "int8", a_scales=sa, b_scales=sb, output_dtype=out, **call_kw)
     view = torch.int16 if out != torch.float32 else torch.int32
     assert torch.equal(plain.view(view), y.view(view))
+
+
+# Shapes the mixed launch takes on 256 CUs (tail tile rows as 256 x 128 tiles): 624 tiles with
+# the last 7 tile rows halved (2 whole rounds + 224 half tiles), 128 tiles all halved, a ragged
+# 300 x 200 output (2 tile rows, the second 128-column tile 72 wide) and 1000 x 600 (K of 3
+# stages less 32 bytes).
+_MIXED_CASES = [(9914, 4096, 256), (2048, 4096, 320), (300, 200, 64), (1000, 600, 352)]
+
+
+@pytest.mark.parametrize("shape", _MIXED_CASES)
+@pytest.mark.parametrize("epilogue", ["bf16", "fp32", "fp16", "bias", "bias_table", "gate", "gate_table", "acc"])
+def test_mixed_tiles_bit_identical_to_plain(shape, epilogue, monkeypatch, device):
+    """Every output element of the mixed launch is one workgroup's dot product over all of K,
+    like the plain launch's, so the two agree bit for bit in every epilogue."""
+    m, n, k = shape
+    g = torch.Generator(device="cpu").manual_seed(m + n + k)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
+    sa = (torch.rand(m, generator=g) * 0.01 + 1e-3).to(device)
+    sb = (torch.rand(n, generator=g) * 0.01 + 1e-3).to(device)
+    out = {"fp32": torch.float32, "fp16": torch.float16}.get(epilogue, torch.bfloat16)
+    rows = torch.tensor([(5 * i) % 3 for i in range(m)], dtype=torch.int32, device=device)
+    kw = {}
+    if epilogue.startswith("bias"):
+        kw["bias"] = torch.randn((3, n) if epilogue == "bias_table" else (n,), generator=g).to(device)
+        kw["bias_map"] = rows if epilogue == "bias_table" else None
+    elif epilogue.startswith("gate"):
+        kw["residual"] = torch.randn((m, n), generator=g).to(torch.bfloat16).to(device)
+        kw["gate"] = torch.randn((3, n) if epilogue == "gate_table" else (n,), generator=g).to(torch.bfloat16).to(device)
+        kw["gate_map"] = rows if epilogue == "gate_table" else None
+
+    def run():
+        if epilogue == "acc":
+            return gemm_i8_accumulators(a, b)
+        return _gemm_i8_call("m5k_gemm_i8", a, b, sa, sb, out, **kw)
+
+    monkeypatch.delenv("M5K_GEMM_MIXED_TILES", raising=False)
+    mixed = run()
+    monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
+    plain = run()
+    view = torch.int16 if mixed.element_size() == 2 else torch.int32
+    assert torch.equal(mixed.view(view), plain.view(view))
+
+
+@pytest.mark.parametrize("shape", _MIXED_CASES)
+@pytest.mark.parametrize("mode", ["bf16", "fp16", "fp32", "fp8"])
+def test_mixed_tiles_float_modes_bit_identical(shape, mode, monkeypatch, device):
+    m, n, k = shape
+    if mode == "fp8":
+        k = -(-k // 128) * 128  # FP8 rows are whole 128-byte stages
+    rng = np.random.default_rng(m + k)
+    a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device)
+    b = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device)
+    if mode == "fp8":
+        (a, sa), (b, sb) = quantize(a.to(torch.bfloat16), "fp8"), quantize(b.to(torch.bfloat16), "fp8")
+        kw = dict(a_scales=sa, b_scales=sb, output_dtype=torch.bfloat16)
+    else:
+        dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[mode]
+        a, b = a.to(dt), b.to(dt)
+        kw = dict(output_dtype=dt)
+    monkeypatch.delenv("M5K_GEMM_MIXED_TILES", raising=False)
+    mixed = gemm(a, b, mode, **kw)
+    monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
+    plain = gemm(a, b, mode, **kw)
+    view = torch.int16 if mixed.element_size() == 2 else torch.int32
+    assert torch.equal(mixed.view(view), plain.view(view))
