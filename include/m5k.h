@@ -130,6 +130,17 @@ int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, i
                        int64_t workspace_elems, void* stream);
 
 /*
+ * Launch plan of the MFMA GEMMs (host only, launches nothing).  No counterpart in the
+ * reference; it lets a host scheduler compose with the library's own choice.  For an
+ * [m,n] output on a device of `cus` compute units, *full_tiles receives the number of
+ * 256 x 256 tiles the mixed launch keeps (the leading whole rounds; every other tile runs
+ * as two 256 x 128 halves in the same launch), or -1 when the plain launch is used.
+ * Every m5k_gemm_* entry point makes this choice with the device's CU count; the result
+ * is bit-identical either way.  M5K_GEMM_MIXED_TILES=0 in the environment forces -1.
+ */
+int m5k_gemm_mixed_plan(int64_t m, int64_t n, int cus, int64_t* full_tiles);
+
+/*
  * Raw INT32 accumulators of the W8A8 GEMM (test hook for bit-exact parity):
  * acc[m,n] = sum_k a[m,k]*b[n,k].  Same kernel main loop as m5k_gemm_i8.
  */

@@ -42,6 +42,14 @@ extern "C" int m5k_gemm_i8_acc(const int8_t* a, const int8_t* b, int64_t m, int6
   return launch<I8, M5K_I32, EPI_NONE, EPI_NONE, true>(a, b, m, n, k, p, as_stream(stream), name);
 }
 
+extern "C" int m5k_gemm_mixed_plan(int64_t m, int64_t n, int cus, int64_t* full_tiles) {
+  clear_error();
+  M5K_REQUIRE(full_tiles != nullptr, "m5k_gemm_mixed_plan: null output");
+  if (int rc = check_shape(m, n, 1, "m5k_gemm_mixed_plan")) return rc;
+  M5K_REQUIRE(cus > 0, "m5k_gemm_mixed_plan: cus must be positive");
+  *full_tiles = mixed_full_tiles(m, n, cus);
+  return M5K_OK;
+}
 
 extern "C" int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
                                   const float* a_scales, const float* b_scales, void* c, int c_dtype,

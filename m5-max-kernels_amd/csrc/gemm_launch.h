@@ -136,37 +136,38 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint
 // ---- Mixed tiles for a partial last round ---------------------------------------------------
 //
 // T tiles on C CUs (one workgroup per CU) take ceil(T / C) rounds; when the last round is only
-// partly filled, most CUs idle through it.  The mixed launch keeps the leading tile rows as
-// 256 x 256 tiles and runs the last `tail` tile rows as 256 x 128 tiles, which take a little
-// over half as long, so the last round is shorter and better filled.  Each output element is
-// still one workgroup's dot product over all of K: results are bit-identical to the plain
-// launch.  Workgroups [0, full) are the 256 x 256 tiles of rows [0, rows_full); the 256 x 128
-// tiles of rows [rows_full, M) start at `full` rounded up to a multiple of 8, so both parts keep
-// the XCD-contiguous numbering of tile_coords (the workgroups in between exit at once).
+// partly filled, most CUs idle through it.  The mixed launch runs the first `full` tiles of the
+// raster order (a whole number of rounds) as 256 x 256 tiles and splits each remaining tile
+// into two 256 x 128 halves, which take a little over half a tile's time each, so the leftover
+// work runs as one shorter, better-filled round.  Each output element is still one
+// workgroup's dot product over all of K: results are bit-identical to the plain launch.
+// Workgroups [0, full) are the full tiles; workgroup full + h is half h & 1 of tile
+// full + h / 2 (full is a multiple of 8, so both parts keep the XCD-contiguous numbering of
+// tile_coords and the two halves of a tile land on one XCD).
 using HalfGrid = Grid8Half;
 
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
 __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_mixed_kernel(const uint8_t* __restrict__ A,
                                                                             const uint8_t* __restrict__ B, int M,
-                                                                            int N, int64_t Kb, int rows_full,
+                                                                            int N, int64_t Kb, int full,
                                                                             EpiParams p) {
-  const int tiles_n = (N + BN - 1) / BN;
-  const int full = rows_full / BM * tiles_n;
-  const int half0 = (full + 7) & ~7;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int bid = static_cast<int>(blockIdx.x);
   if (bid < full) {
     using G = KernelGrid;
     int tm, tn;
-    tile_coords(bid, rows_full / BM, tiles_n, tm, tn);
+    band_coords(xcd_logical(bid, full), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     AccTile<MODE, G> acc;
     mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
     epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
-  } else if (bid >= half0) {
+  } else {
     using G = HalfGrid;
+    const int h = xcd_logical(bid - full, 2 * (tiles_m * tiles_n - full));
     int tm, tn;
-    tile_coords(bid - half0, (M - rows_full + BM - 1) / BM, (N + G::TN - 1) / G::TN, tm, tn);
-    const int m0 = rows_full + tm * BM, n0 = tn * G::TN;
+    band_coords(full + (h >> 1), tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN + (h & 1) * G::TN;
+    if (n0 >= N) return;  // right half of a last tile column at most 128 wide (whole workgroup)
     AccTile<MODE, G> acc;
     mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
     epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
@@ -174,79 +175,43 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_mixed_kernel(cons
 }
 
 constexpr int XCDS = 8;
-// Time of a 256 x 128 tile in units of a 256 x 256 tile's.
+// Time of a 256 x 128 tile in units of a 256 x 256 tile's (measured: 256 half tiles of
+// 2048 x 4096 x 4096 INT8 in 0.57 of the 256 full tiles of 4096 x 4096 x 4096).
 constexpr double kHalfTileCost = 0.56;
 
-// Finish time, in 256 x 256 tile times, of one XCD running nf full tiles and then nh half
-// tiles on c CUs, each workgroup taken in order by the first free CU.
-inline double xcd_makespan(int64_t nf, int64_t nh, int c, double h) {
-  const int64_t F = nf / c, L = nf % c;  // L CUs run one more full tile than the other c - L
-  double end = L ? F + 1.0 : static_cast<double>(F);
-  if (nh == 0) return end;
-  // Half-tile slots open at F + i h on c - L CUs and at F + 1 + j h on L CUs; the jobs take the
-  // earliest nh of them.
-  int64_t i = 0, j = 0, left = nh;
-  double last = 0.0;
-  while (left > 0) {
-    const double t1 = F + i * h, t2 = F + 1.0 + j * h;
-    if (c - L > 0 && (L == 0 || t1 <= t2)) {
-      left -= c - L < left ? c - L : left;
-      last = t1;
-      ++i;
-    } else {
-      left -= L < left ? L : left;
-      last = t2;
-      ++j;
-    }
-  }
-  return end > last + h ? end : last + h;
-}
-
+// Finish time, in 256 x 256 tile times, of `full` tiles (a multiple of the CU count: whole
+// rounds) followed by `half` half tiles; workgroup w runs on XCD w % 8, whose CUs take its
+// workgroups in order.
 inline double mixed_makespan(int64_t full, int64_t half, int cus) {
-  const int c = cus / XCDS;
-  double worst = 0.0;
-  for (int x = 0; x < XCDS; ++x) {
-    const int64_t nf = full / XCDS + (x < full % XCDS), nh = half / XCDS + (x < half % XCDS);
-    const double t = xcd_makespan(nf, nh, c, kHalfTileCost);
-    worst = t > worst ? t : worst;
-  }
-  return worst;
+  const int64_t c = cus / XCDS;
+  const int64_t per = (half + XCDS - 1) / XCDS;  // the busiest XCD's half tiles
+  return static_cast<double>(full / cus) + static_cast<double>((per + c - 1) / c) * kHalfTileCost;
 }
 
-// Tile rows to run as 256 x 128 tiles (0: the plain launch), chosen by the makespan model
-// above and used only for a predicted gain of 5% or more.  The full-tile part must fill whole
-// rounds (or be empty), so the half tiles start together once every full tile is done:
-// measured on MI355X, half tiles that overlap a partial round of full tiles ran slower than
-// the model (N = 6144 at 1.5 rounds and N = 14336 at 3.5 rounds lost 4-8% against the plain
-// launch), while the whole-round splits matched or beat it (M = 9914, 4352, 2048, 1024).
-// M5K_GEMM_MIXED_TILES=0 in the environment turns the mixed launch off (read on every call).
-inline int64_t mixed_tail_rows(int64_t m, int64_t n, int cus) {
-  if (cus < XCDS) return 0;
-  if (const char* env = std::getenv("M5K_GEMM_MIXED_TILES"); env && env[0] == '0') return 0;
-  const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
-  const int64_t tiles_nh = (n + HalfGrid::TN - 1) / HalfGrid::TN;
-  if (tiles_m * tiles_n > 64 * static_cast<int64_t>(cus)) return 0;  // a partial round is noise
-  struct Entry {
-    int64_t m_tiles, n, cus, rows;
-  };
-  static thread_local Entry memo[16] = {};
-  Entry& e = memo[(tiles_m * 31 + n * 7 + cus) & 15];
-  if (e.m_tiles == tiles_m && e.n == n && e.cus == cus) return e.rows;
-  const double plain = mixed_makespan(tiles_m * tiles_n, 0, cus);
-  // Only the rows of about one round are worth converting.
-  const int64_t max_rows = std::min<int64_t>(tiles_m, (cus + tiles_n - 1) / tiles_n + 1);
-  double best = plain * 0.95;
-  int64_t rows = 0;
-  for (int64_t r = 1; r <= max_rows; ++r) {
-    if ((tiles_m - r) * tiles_n % cus != 0) continue;
-    const double t = mixed_makespan((tiles_m - r) * tiles_n, r * tiles_nh, cus);
+// Full tiles of the mixed launch, or -1 for the plain launch.  Candidates keep the last one
+// or two rounds of tiles as halves; the mixed launch is used for a predicted gain of 5% or
+// more.  The full part is always whole rounds, so the half tiles start together once every
+// full tile is done.  Measured on MI355X, half tiles that overlapped a partial round of full
+// tiles ran slower than such a model predicts (4-8% behind the plain launch at N = 6144 and
+// 14336), while the whole-round splits matched or beat it.
+// M5K_GEMM_MIXED_TILES=0 in the environment selects the plain launch (read on every call).
+inline int64_t mixed_full_tiles(int64_t m, int64_t n, int cus) {
+  if (cus < XCDS || cus % XCDS) return -1;
+  if (const char* env = std::getenv("M5K_GEMM_MIXED_TILES"); env && env[0] == '0') return -1;
+  const int64_t total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  const int64_t rounds = total / cus;
+  if (total % cus == 0 || rounds > 64) return -1;  // no partial round, or one that is noise
+  double best = static_cast<double>(rounds + 1) * 0.95;
+  int64_t pick = -1;
+  for (int64_t j = rounds; j >= 0 && j + 2 >= rounds; --j) {
+    const int64_t full = j * cus;
+    const double t = mixed_makespan(full, 2 * (total - full), cus);
     if (t < best) {
       best = t;
-      rows = r;
+      pick = full;
     }
   }
-  e = Entry{tiles_m, n, cus, rows};
-  return rows;
+  return pick;
 }
 
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
@@ -264,12 +229,10 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   EpiParams q = p;
   q.coalesced = n % 8 == 0 && aligned16(p.c) && (p.residual == nullptr || (aligned16(p.residual) && aligned16(p.gate)));
   if (aligned) {
-    if (const int64_t tail = mixed_tail_rows(m, n, device_cus())) {
-      const int64_t tiles_m = (m + BM - 1) / BM, tiles_n = (n + BN - 1) / BN;
-      const int64_t full = (tiles_m - tail) * tiles_n;
-      const int64_t wgs = (full + 7) / 8 * 8 + tail * ((n + HalfGrid::TN - 1) / HalfGrid::TN);
+    if (const int64_t full = mixed_full_tiles(m, n, device_cus()); full >= 0) {
+      const int64_t wgs = full + 2 * (tiles - full);
       gemm_mixed_kernel<MODE, OUT_DT, BIAS, GATE, RAW><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(
-          A, B, (int)m, (int)n, kb, static_cast<int>((tiles_m - tail) * BM), q);
+          A, B, (int)m, (int)n, kb, static_cast<int>(full), q);
     } else {
       gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
     }

@@ -18,6 +18,8 @@ Differences that follow from the platform, not the contract:
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -129,6 +131,14 @@ def tail_split_plan(m, n, k, cus=256):
         if gain > best_gain:
             best, best_gain = splits, gain
     return None if best is None else (rows_dp * 256, best)
+
+
+def mixed_plan(m, n, cus=256):
+    """256 x 256 tiles the library's mixed launch keeps for an [m, n] output, or -1 when it
+    uses the plain launch (m5k_gemm_mixed_plan; host only)."""
+    full = ctypes.c_int64(0)
+    _lib.call("m5k_gemm_mixed_plan", m, n, cus, ctypes.byref(full))
+    return full.value
 
 
 def _cu_count(device):
@@ -251,7 +261,10 @@ def gemm(
             bias_row_map = None if bias_row_map is None else _lib.device_tensor(bias_row_map, "bias_row_map")
         aligned = k % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
         splits = splitk_plan(m, n, k) if aligned else 1
-        tail = tail_split_plan(m, n, k, _cu_count(a.device)) if aligned and splits == 1 else None
+        # The library's mixed launch refills a partial last round without INT32 partials and
+        # measured faster wherever both apply; the split-K tail takes the rest.
+        cus = _cu_count(a.device) if aligned and splits == 1 else 0
+        tail = tail_split_plan(m, n, k, cus) if cus and mixed_plan(m, n, cus) < 0 else None
         if tail is not None:
             # Whole tile rows in full rounds, then the remaining rows split along K.  Every
             # row-indexed operand is sliced at the same row; both launches are bit-exact.

@@ -199,6 +199,37 @@ def test_shift_split_validation():
         shift_split_condition(g, g, g, w)
 
 
+def test_mixed_plan_decisions(monkeypatch):
+    """The library's launch plan on 256 CUs (host query, no GPU): whole rounds keep the plain
+    launch; a partial last round keeps the leading whole rounds as 256 x 256 tiles and halves
+    the rest when one shorter round saves 5% or more (measured 6-22% faster on MI355X at these
+    shapes, bit-identical); tails that stay over half a round, and 8+ rounds, stay plain."""
+    from m5kernels_amd.hip import mixed_plan
+
+    expected = {
+        (4096, 4096): -1,     # 256 tiles: one whole round
+        (4096, 7168): -1,     # 448 tiles: halving 192 leftover tiles needs two half rounds
+        (9914, 14336): -1,    # 2184 tiles: 8.5 rounds
+        (9914, 4096): 512,    # 624 tiles: 2 rounds + 224 halves
+        (4096, 5376): 256,    # 336 tiles: 1 round + 160 halves
+        (4096, 14336): 768,   # 896 tiles: 3 rounds + 256 halves
+        (2048, 4096): 0,      # 128 tiles: all halved
+        (300, 200): 0,
+    }
+    for (m, n), full in expected.items():
+        assert mixed_plan(m, n, 256) == full, (m, n)
+    for m in range(1, 12000, 331):
+        for n in (96, 1536, 4096, 5376, 7168):
+            full = mixed_plan(m, n, 256)
+            tiles = -(-m // 256) * -(-n // 256)
+            assert full == -1 or (full % 256 == 0 and 0 <= full < tiles and tiles % 256)
+    monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
+    assert mixed_plan(9914, 4096, 256) == -1
+    monkeypatch.delenv("M5K_GEMM_MIXED_TILES")
+    with pytest.raises(RuntimeError, match="cus must be positive"):
+        mixed_plan(9914, 4096, 0)
+
+
 def test_tail_split_plan_decisions():
     """Host schedule of the W8A8 linear on 256 CUs: the row split is taken where the measured
     cost model says it pays (H3 widths at M 4096) and declined where it does not (M 9914 x

@@ -332,10 +332,11 @@ def test_splitk_plan_and_routing(device):
 
 
 
-# Shapes with a partial last round that gemm() splits by rows (256 CUs): 336 tiles (tail rows
-# 1024, 3 K ranges), 272 tiles (tail rows 256, 4 ranges), 288 tiles with a ragged last tile
-# row (tail rows 304).
-_TAIL_CASES = [(4096, 5376, 5376), (4352, 4096, 2048), (4400, 4096, 2048)]
+# Shapes of 8+ rounds with a partial last round that gemm() splits by rows (256 CUs; the
+# library's mixed launch declines them, one shorter round saving under 5%): 2072 tiles (tail
+# rows 256, 5 K ranges), 2064 tiles (tail rows 256, 6 ranges), 2080 tiles with a ragged last
+# tile row (tail rows 332, 5 ranges).
+_TAIL_CASES = [(18944, 7168, 4096), (33024, 4096, 4096), (33100, 4096, 4096)]
 
 
 @pytest.mark.parametrize("shape", _TAIL_CASES)
@@ -344,13 +345,13 @@ def test_tail_split_bit_identical_to_plain(shape, epilogue, device):
     """gemm() runs whole tile rows as a plain launch and the rest as split-K, slicing every
     row-indexed operand (scales, row maps, residual, output) at the same row; the result
     matches one plain m5k_gemm_i8 launch bit for bit."""
-    from m5kernels_amd.hip import tail_split_plan
+    from m5kernels_amd.hip import mixed_plan, tail_split_plan
 
     m, n, k = shape
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if cus != 256:
         pytest.skip("shapes chosen for 256 CUs")
-    assert tail_split_plan(m, n, k, cus) is not None
+    assert tail_split_plan(m, n, k, cus) is not None and mixed_plan(m, n, cus) < 0
     g = torch.Generator(device="cpu").manual_seed(m + n + k)
     a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
     b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
@@ -374,11 +375,11 @@ def test_tail_split_bit_identical_to_plain(shape, epilogue, device):
     assert torch.equal(plain.view(view), y.view(view))
 
 
-# Shapes the mixed launch takes on 256 CUs (tail tile rows as 256 x 128 tiles): 624 tiles with
-# the last 7 tile rows halved (2 whole rounds + 224 half tiles), 128 tiles all halved, a ragged
-# 300 x 200 output (2 tile rows, the second 128-column tile 72 wide) and 1000 x 600 (K of 3
-# stages less 32 bytes).
-_MIXED_CASES = [(9914, 4096, 256), (2048, 4096, 320), (300, 200, 64), (1000, 600, 352)]
+# Shapes the mixed launch takes on 256 CUs: 624 tiles (2 rounds + 224 halves), 128 tiles (all
+# halved), a ragged 300 x 200 output (the second half of its one tile 72 wide), 1000 x 600
+# (the right halves of the 88-wide last tile column exit at once) and 4096 x 5376 (a round of
+# 256 tiles that ends inside a 4-row raster band, + 160 halves; K of 1.5 stages).
+_MIXED_CASES = [(9914, 4096, 256), (2048, 4096, 320), (300, 200, 64), (1000, 600, 352), (4096, 5376, 192)]
 
 
 @pytest.mark.parametrize("shape", _MIXED_CASES)
