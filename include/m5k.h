@@ -132,13 +132,19 @@ int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, i
 /*
  * Launch plan of the MFMA GEMMs (host only, launches nothing).  No counterpart in the
  * reference; it lets a host scheduler compose with the library's own choice.  For an
- * [m,n] output on a device of `cus` compute units, *full_tiles receives the number of
- * 256 x 256 tiles the mixed launch keeps (the leading whole rounds; every other tile runs
- * as two 256 x 128 halves in the same launch), or -1 when the plain launch is used.
- * Every m5k_gemm_* entry point makes this choice with the device's CU count; the result
- * is bit-identical either way.  M5K_GEMM_MIXED_TILES=0 in the environment forces -1.
+ * [m,n] output with operands of ab_dtype (M5K_I8, M5K_U8 for FP8 codes, M5K_BF16, M5K_F16,
+ * M5K_F32) on a device of `cus` compute units, *schedule receives
+ *   0  plain: 256 x 256 tiles;
+ *   1  mixed: the leading *full_tiles 256 x 256 tiles (whole rounds), every other tile as
+ *      two 256 x 128 halves in the same launch;
+ *   2  narrow: 256 x 224 tiles (I8 / BF16 / F16 only);
+ * and *full_tiles is -1 unless the schedule is 1.  Every m5k_gemm_* entry point makes this
+ * choice with the device's CU count for operands on the direct-to-LDS path (row bytes a
+ * multiple of 16, 16-byte aligned bases); the others run the plain schedule.  Results are
+ * bit-identical under every schedule.  M5K_GEMM_MIXED_TILES=0 / M5K_GEMM_NARROW_TILES=0 in
+ * the environment switch schedule 1 / 2 off.
  */
-int m5k_gemm_mixed_plan(int64_t m, int64_t n, int cus, int64_t* full_tiles);
+int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus, int* schedule, int64_t* full_tiles);
 
 /*
  * Raw INT32 accumulators of the W8A8 GEMM (test hook for bit-exact parity):

@@ -53,8 +53,9 @@ constexpr int GROUP_M = 4;             // tile-rows per raster band
 // (256/WAVES_N) sub-tile of MFMA blocks.  2 x 2 = one wave per SIMD with 256 accumulator
 // registers; 2 x 4 = two waves per SIMD with 128 each, so one wave's MFMAs keep the pipe busy
 // while its sibling waits at a barrier.
-// TN is the tile's column count: BN for the full tile, BN / 2 for the half-width tiles that
-// refill a partial last round.
+// TN is the tile's column count: BN for the full tile, less for the narrower tiles that refill
+// a partial last round or make the tile count a whole number of rounds.  B rows are moved in
+// whole 16-row groups per wave; rows past TN load nothing (their LDS rows are never read).
 template <int WAVES_M_, int WAVES_N_, int TN_ = BN>
 struct Grid {
   static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
@@ -64,12 +65,13 @@ struct Grid {
   static constexpr int WM = BM / WAVES_M, WN = TN / WAVES_N;
   static constexpr int DMA_ROWS = BM / WAVES;       // A rows one wave DMAs per stage
   static constexpr int DMA_INSTR = DMA_ROWS / 8;    // 1 KiB (8 rows of 128 B) per instruction
-  static constexpr int DMA_ROWS_B = TN / WAVES;     // B rows one wave DMAs per stage
+  static constexpr int DMA_ROWS_B = (TN / WAVES + 15) / 16 * 16;  // B rows one wave DMAs per stage
   static constexpr int DMA_INSTR_B = DMA_ROWS_B / 8;
 };
 using Grid4 = Grid<2, 2>;
 using Grid8 = Grid<2, 4>;
-using Grid8Half = Grid<4, 2, BN / 2>;  // 256 x 128 tile, 8 waves of 64 x 64
+using Grid8Half = Grid<4, 2, BN / 2>;     // 256 x 128 tile, 8 waves of 64 x 64
+using Grid8Narrow = Grid<4, 2, 7 * BN / 8>;  // 256 x 224 tile, 8 waves of 64 x 112 (16 x 16 modes)
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <int MODE>
@@ -407,7 +409,8 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
 #pragma unroll
   for (int i = 0; i < G::DMA_INSTR_B; ++i) {
     const int r = wave * G::DMA_ROWS_B + 8 * i + (lane >> 3);
-    b_base[i] = tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb) + lchunk[i & 1] : kOob;
+    b_base[i] = r < G::TN && tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb) + lchunk[i & 1]
+                                             : kOob;
   }
   const uint32_t lds_row0 = static_cast<uint32_t>(uwave * G::DMA_ROWS * BKB);
   const uint32_t lds_row0_b = static_cast<uint32_t>(uwave * G::DMA_ROWS_B * BKB);

@@ -42,12 +42,18 @@ extern "C" int m5k_gemm_i8_acc(const int8_t* a, const int8_t* b, int64_t m, int6
   return launch<I8, M5K_I32, EPI_NONE, EPI_NONE, true>(a, b, m, n, k, p, as_stream(stream), name);
 }
 
-extern "C" int m5k_gemm_mixed_plan(int64_t m, int64_t n, int cus, int64_t* full_tiles) {
+extern "C" int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus, int* schedule,
+                                    int64_t* full_tiles) {
   clear_error();
-  M5K_REQUIRE(full_tiles != nullptr, "m5k_gemm_mixed_plan: null output");
-  if (int rc = check_shape(m, n, 1, "m5k_gemm_mixed_plan")) return rc;
-  M5K_REQUIRE(cus > 0, "m5k_gemm_mixed_plan: cus must be positive");
-  *full_tiles = mixed_full_tiles(m, n, cus);
+  const char* name = "m5k_gemm_launch_plan";
+  M5K_REQUIRE(schedule != nullptr && full_tiles != nullptr, "%s: null output", name);
+  if (int rc = check_shape(m, n, 1, name)) return rc;
+  M5K_REQUIRE(cus > 0, "%s: cus must be positive", name);
+  M5K_REQUIRE(ab_dtype == M5K_I8 || ab_dtype == M5K_U8 || ab_dtype == M5K_BF16 || ab_dtype == M5K_F16 ||
+                  ab_dtype == M5K_F32,
+              "%s: ab_dtype must be I8, U8 (FP8 codes), BF16, F16 or F32", name);
+  const bool md16 = ab_dtype == M5K_I8 || ab_dtype == M5K_BF16 || ab_dtype == M5K_F16;
+  *schedule = plan_schedule(md16, m, n, cus, *full_tiles);
   return M5K_OK;
 }
 

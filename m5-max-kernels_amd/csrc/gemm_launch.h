@@ -118,19 +118,19 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int
   });
 }
 
-template <int MODE, bool ALIGNED, int OUT_DT, int BIAS, int GATE, bool RAW>
-__global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
-                                                                      const uint8_t* __restrict__ B, int M, int N,
-                                                                      int64_t Kb, EpiParams p) {
-  using G = KernelGrid;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+// One 256 x G::TN output tile per workgroup.
+template <int MODE, bool ALIGNED, int OUT_DT, int BIAS, int GATE, bool RAW, class G = KernelGrid>
+__global__ __launch_bounds__(G::THREADS, 1) void gemm_kernel(const uint8_t* __restrict__ A,
+                                                             const uint8_t* __restrict__ B, int M, int N,
+                                                             int64_t Kb, EpiParams p) {
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + G::TN - 1) / G::TN;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM, n0 = tn * G::TN;
   AccTile<MODE, G> acc;
   if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
-  epilogue<MODE, OUT_DT, BIAS, GATE, RAW>(acc, M, N, m0, n0, p);
+  epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
 }
 
 // ---- Mixed tiles for a partial last round ---------------------------------------------------
@@ -214,6 +214,43 @@ inline int64_t mixed_full_tiles(int64_t m, int64_t n, int cus) {
   return pick;
 }
 
+// ---- Narrow tiles for a whole number of rounds ------------------------------------------------
+//
+// 256 x 224 tiles (Grid8Narrow, 16 x 16 modes) do 7/8 of a full tile's MFMAs.  Where their
+// count fills whole rounds and the 256-wide count does not (N = 7168: 28 full or 32 narrow
+// tile columns; at M = 4096, 448 tiles = 1.75 rounds against 512 = 2 rounds), the narrow grid
+// finishes in 2 x 7/8 round times instead of 2.  Bit-identical to the plain launch for the
+// same reason as the mixed launch.
+constexpr double kNarrowTileCost = 0.9;  // 256 x 224 tile time / 256 x 256 tile time
+
+// Predicted time, in 256 x 256 tile times, of the plain, mixed and narrow launches; returns
+// true when the narrow launch is 5% or more ahead of both others.
+inline bool narrow_pays(int64_t m, int64_t n, int cus, int64_t mixed_full) {
+  if (cus <= 0) return false;
+  if (const char* env = std::getenv("M5K_GEMM_NARROW_TILES"); env && env[0] == '0') return false;
+  const int64_t tiles_m = (m + BM - 1) / BM;
+  const int64_t plain_tiles = tiles_m * ((n + BN - 1) / BN);
+  const int64_t narrow_tiles = tiles_m * ((n + Grid8Narrow::TN - 1) / Grid8Narrow::TN);
+  if (plain_tiles > 64 * static_cast<int64_t>(cus)) return false;
+  double other = static_cast<double>((plain_tiles + cus - 1) / cus);
+  if (mixed_full >= 0) other = std::min(other, mixed_makespan(mixed_full, 2 * (plain_tiles - mixed_full), cus));
+  const double narrow = static_cast<double>((narrow_tiles + cus - 1) / cus) * kNarrowTileCost;
+  return narrow < 0.95 * other;
+}
+
+enum Schedule { SCHED_PLAIN = 0, SCHED_MIXED = 1, SCHED_NARROW = 2 };
+
+// Launch schedule of an aligned GEMM with an [m, n] output on `cus` CUs; `full` receives the
+// mixed launch's full tiles (-1 otherwise).  Narrow tiles exist for the 16 x 16 modes only.
+inline int plan_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& full) {
+  full = mixed_full_tiles(m, n, cus);
+  if (md16 && narrow_pays(m, n, cus, full)) {
+    full = -1;
+    return SCHED_NARROW;
+  }
+  return full >= 0 ? SCHED_MIXED : SCHED_PLAIN;
+}
+
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
 int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
            hipStream_t st, const char* name) {
@@ -229,7 +266,18 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   EpiParams q = p;
   q.coalesced = n % 8 == 0 && aligned16(p.c) && (p.residual == nullptr || (aligned16(p.residual) && aligned16(p.gate)));
   if (aligned) {
-    if (const int64_t full = mixed_full_tiles(m, n, device_cus()); full >= 0) {
+    int64_t full = -1;
+    const int sched = plan_schedule(Traits<MODE>::MD == 16, m, n, device_cus(), full);
+    if constexpr (Traits<MODE>::MD == 16) {
+      if (sched == SCHED_NARROW) {
+        using G = Grid8Narrow;
+        const int64_t wgs = ((m + BM - 1) / BM) * ((n + G::TN - 1) / G::TN);
+        gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW, G><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(
+            A, B, (int)m, (int)n, kb, q);
+        return launch_status(name);
+      }
+    }
+    if (sched == SCHED_MIXED) {
       const int64_t wgs = full + 2 * (tiles - full);
       gemm_mixed_kernel<MODE, OUT_DT, BIAS, GATE, RAW><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(
           A, B, (int)m, (int)n, kb, static_cast<int>(full), q);

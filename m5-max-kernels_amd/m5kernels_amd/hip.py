@@ -133,12 +133,16 @@ def tail_split_plan(m, n, k, cus=256):
     return None if best is None else (rows_dp * 256, best)
 
 
-def mixed_plan(m, n, cus=256):
-    """256 x 256 tiles the library's mixed launch keeps for an [m, n] output, or -1 when it
-    uses the plain launch (m5k_gemm_mixed_plan; host only)."""
-    full = ctypes.c_int64(0)
-    _lib.call("m5k_gemm_mixed_plan", m, n, cus, ctypes.byref(full))
-    return full.value
+_PLAN_DTYPES = {"int8": _lib.I8, "fp8": _lib.U8, "bf16": _lib.BF16, "fp16": _lib.F16, "fp32": _lib.F32}
+SCHEDULES = ("plain", "mixed", "narrow")
+
+
+def launch_plan(mode, m, n, cus=256):
+    """The library's GEMM schedule for an [m, n] output on `cus` CUs (m5k_gemm_launch_plan;
+    host only): ("plain" | "mixed" | "narrow", full tiles of the mixed launch or -1)."""
+    sched, full = ctypes.c_int(0), ctypes.c_int64(0)
+    _lib.call("m5k_gemm_launch_plan", _PLAN_DTYPES[mode], m, n, cus, ctypes.byref(sched), ctypes.byref(full))
+    return SCHEDULES[sched.value], full.value
 
 
 def _cu_count(device):
@@ -261,10 +265,10 @@ def gemm(
             bias_row_map = None if bias_row_map is None else _lib.device_tensor(bias_row_map, "bias_row_map")
         aligned = k % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
         splits = splitk_plan(m, n, k) if aligned else 1
-        # The library's mixed launch refills a partial last round without INT32 partials and
-        # measured faster wherever both apply; the split-K tail takes the rest.
+        # The library's mixed and narrow launches refill a partial last round without INT32
+        # partials and measured faster wherever both apply; the split-K tail takes the rest.
         cus = _cu_count(a.device) if aligned and splits == 1 else 0
-        tail = tail_split_plan(m, n, k, cus) if cus and mixed_plan(m, n, cus) < 0 else None
+        tail = tail_split_plan(m, n, k, cus) if cus and launch_plan("int8", m, n, cus)[0] == "plain" else None
         if tail is not None:
             # Whole tile rows in full rounds, then the remaining rows split along K.  Every
             # row-indexed operand is sliced at the same row; both launches are bit-exact.

@@ -199,35 +199,50 @@ def test_shift_split_validation():
         shift_split_condition(g, g, g, w)
 
 
-def test_mixed_plan_decisions(monkeypatch):
-    """The library's launch plan on 256 CUs (host query, no GPU): whole rounds keep the plain
-    launch; a partial last round keeps the leading whole rounds as 256 x 256 tiles and halves
-    the rest when one shorter round saves 5% or more (measured 6-22% faster on MI355X at these
-    shapes, bit-identical); tails that stay over half a round, and 8+ rounds, stay plain."""
-    from m5kernels_amd.hip import mixed_plan
+def test_launch_plan_decisions(monkeypatch):
+    """The library's GEMM schedule on 256 CUs (host query, no GPU).  Whole rounds keep the plain
+    launch.  A partial last round keeps the leading whole rounds as 256 x 256 tiles and halves
+    the rest when one shorter round saves 5% or more.  256 x 224 tiles (16 x 16 modes) take
+    shapes whose narrow tile count fills whole rounds.  Every choice here measured faster on
+    MI355X than the plain launch (mixed 6-22%, narrow 3-6%), bit-identically."""
+    from m5kernels_amd.hip import launch_plan
 
     expected = {
-        (4096, 4096): -1,     # 256 tiles: one whole round
-        (4096, 7168): -1,     # 448 tiles: halving 192 leftover tiles needs two half rounds
-        (9914, 14336): -1,    # 2184 tiles: 8.5 rounds
-        (9914, 4096): 512,    # 624 tiles: 2 rounds + 224 halves
-        (4096, 5376): 256,    # 336 tiles: 1 round + 160 halves
-        (4096, 14336): 768,   # 896 tiles: 3 rounds + 256 halves
-        (2048, 4096): 0,      # 128 tiles: all halved
-        (300, 200): 0,
+        (4096, 4096): ("plain", -1),     # 256 tiles: one whole round
+        (9914, 14336): ("plain", -1),    # 2184 tiles: 8.5 rounds
+        (9914, 4096): ("mixed", 512),    # 624 tiles: 2 rounds + 224 halves
+        (4096, 5376): ("mixed", 256),    # 336 tiles: 1 round + 160 halves
+        (4096, 14336): ("mixed", 768),   # 896 tiles: 3 rounds + 256 halves
+        (2048, 4096): ("mixed", 0),      # 128 tiles: all halved
+        (300, 200): ("mixed", 0),
+        (4096, 7168): ("narrow", -1),    # 448 tiles = 1.75 rounds; 512 narrow tiles = 2 rounds
+        (1024, 14336): ("narrow", -1),   # 224 tiles; 256 narrow tiles
+        (2048, 5120): ("narrow", -1),    # ragged last narrow tile column (5120 = 22 x 224 + 192)
     }
-    for (m, n), full in expected.items():
-        assert mixed_plan(m, n, 256) == full, (m, n)
+    for (m, n), plan in expected.items():
+        assert launch_plan("int8", m, n, 256) == plan, (m, n)
+        assert launch_plan("bf16", m, n, 256) == plan, (m, n)
+    # FP8 and FP32 use 32 x 32 blocks and have no narrow grid.
+    assert launch_plan("fp8", 4096, 7168, 256) == ("plain", -1)
+    assert launch_plan("fp32", 9914, 4096, 256) == ("mixed", 512)
     for m in range(1, 12000, 331):
         for n in (96, 1536, 4096, 5376, 7168):
-            full = mixed_plan(m, n, 256)
+            sched, full = launch_plan("int8", m, n, 256)
             tiles = -(-m // 256) * -(-n // 256)
-            assert full == -1 or (full % 256 == 0 and 0 <= full < tiles and tiles % 256)
+            if sched == "mixed":
+                assert full % 256 == 0 and 0 <= full < tiles and tiles % 256
+            else:
+                assert full == -1
     monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
-    assert mixed_plan(9914, 4096, 256) == -1
+    assert launch_plan("int8", 9914, 4096, 256) == ("narrow", -1)  # 741 narrow tiles: 3 rounds
+    assert launch_plan("fp32", 9914, 4096, 256) == ("plain", -1)
+    monkeypatch.setenv("M5K_GEMM_NARROW_TILES", "0")
+    assert launch_plan("int8", 9914, 4096, 256) == ("plain", -1)
+    assert launch_plan("int8", 4096, 7168, 256) == ("plain", -1)
     monkeypatch.delenv("M5K_GEMM_MIXED_TILES")
+    monkeypatch.delenv("M5K_GEMM_NARROW_TILES")
     with pytest.raises(RuntimeError, match="cus must be positive"):
-        mixed_plan(9914, 4096, 0)
+        launch_plan("int8", 9914, 4096, 0)
 
 
 def test_tail_split_plan_decisions():

@@ -33,12 +33,17 @@ def _codes(m, n, k, seed=83, bound=127):
 @pytest.fixture(params=["auto", "plain"])
 def schedule(request, monkeypatch):
     """Run a test under the library's launch choice ("auto": shapes with a partial last round
-    take the mixed 256 x 256 / 256 x 128 launch) and with that launch switched off."""
-    if request.param == "plain":
-        monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
-    else:
-        monkeypatch.delenv("M5K_GEMM_MIXED_TILES", raising=False)
+    take the mixed 256 x 256 / 256 x 128 launch or 256 x 224 tiles) and with both switched off."""
+    _set_schedule(monkeypatch, request.param)
     return request.param
+
+
+def _set_schedule(monkeypatch, schedule):
+    for var in ("M5K_GEMM_MIXED_TILES", "M5K_GEMM_NARROW_TILES"):
+        if schedule == "plain":
+            monkeypatch.setenv(var, "0")
+        else:
+            monkeypatch.delenv(var, raising=False)
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -345,13 +350,13 @@ def test_tail_split_bit_identical_to_plain(shape, epilogue, device):
     """gemm() runs whole tile rows as a plain launch and the rest as split-K, slicing every
     row-indexed operand (scales, row maps, residual, output) at the same row; the result
     matches one plain m5k_gemm_i8 launch bit for bit."""
-    from m5kernels_amd.hip import mixed_plan, tail_split_plan
+    from m5kernels_amd.hip import launch_plan, tail_split_plan
 
     m, n, k = shape
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if cus != 256:
         pytest.skip("shapes chosen for 256 CUs")
-    assert tail_split_plan(m, n, k, cus) is not None and mixed_plan(m, n, cus) < 0
+    assert tail_split_plan(m, n, k, cus) is not None and launch_plan("int8", m, n, cus)[0] == "plain"
     g = torch.Generator(device="cpu").manual_seed(m + n + k)
     a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
     b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
@@ -378,8 +383,11 @@ def test_tail_split_bit_identical_to_plain(shape, epilogue, device):
 # Shapes the mixed launch takes on 256 CUs: 624 tiles (2 rounds + 224 halves), 128 tiles (all
 # halved), a ragged 300 x 200 output (the second half of its one tile 72 wide), 1000 x 600
 # (the right halves of the 88-wide last tile column exit at once) and 4096 x 5376 (a round of
-# 256 tiles that ends inside a 4-row raster band, + 160 halves; K of 1.5 stages).
-_MIXED_CASES = [(9914, 4096, 256), (2048, 4096, 320), (300, 200, 64), (1000, 600, 352), (4096, 5376, 192)]
+# 256 tiles that ends inside a 4-row raster band, + 160 halves; K of 1.5 stages).  Then shapes
+# that take 256 x 224 tiles (16 x 16 modes): 4096 x 7168 (512 narrow tiles) and 2048 x 5120
+# (a 192-wide last narrow tile column).
+_MIXED_CASES = [(9914, 4096, 256), (2048, 4096, 320), (300, 200, 64), (1000, 600, 352), (4096, 5376, 192),
+                (4096, 7168, 128), (2048, 5120, 320)]
 
 
 @pytest.mark.parametrize("shape", _MIXED_CASES)
@@ -409,9 +417,9 @@ def test_mixed_tiles_bit_identical_to_plain(shape, epilogue, monkeypatch, device
             return gemm_i8_accumulators(a, b)
         return _gemm_i8_call("m5k_gemm_i8", a, b, sa, sb, out, **kw)
 
-    monkeypatch.delenv("M5K_GEMM_MIXED_TILES", raising=False)
+    _set_schedule(monkeypatch, "auto")
     mixed = run()
-    monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
+    _set_schedule(monkeypatch, "plain")
     plain = run()
     view = torch.int16 if mixed.element_size() == 2 else torch.int32
     assert torch.equal(mixed.view(view), plain.view(view))
@@ -433,9 +441,9 @@ def test_mixed_tiles_float_modes_bit_identical(shape, mode, monkeypatch, device)
         dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[mode]
         a, b = a.to(dt), b.to(dt)
         kw = dict(output_dtype=dt)
-    monkeypatch.delenv("M5K_GEMM_MIXED_TILES", raising=False)
+    _set_schedule(monkeypatch, "auto")
     mixed = gemm(a, b, mode, **kw)
-    monkeypatch.setenv("M5K_GEMM_MIXED_TILES", "0")
+    _set_schedule(monkeypatch, "plain")
     plain = gemm(a, b, mode, **kw)
     view = torch.int16 if mixed.element_size() == 2 else torch.int32
     assert torch.equal(mixed.view(view), plain.view(view))
