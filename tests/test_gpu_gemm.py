@@ -447,3 +447,51 @@ def test_mixed_tiles_float_modes_bit_identical(shape, mode, monkeypatch, device)
     plain = gemm(a, b, mode, **kw)
     view = torch.int16 if mixed.element_size() == 2 else torch.int32
     assert torch.equal(mixed.view(view), plain.view(view))
+
+
+def _random_schedule_cases(count_per_schedule=20, seed=2024):
+    """Seeded random [m, n, k, mode] cases, `count_per_schedule` for each of the plain, mixed and
+    narrow schedules (as the library plans them on 256 CUs), with ragged m, n and K."""
+    import random
+
+    from m5kernels_amd.hip import launch_plan
+
+    rng = random.Random(seed)
+    counts = {"plain": 0, "mixed": 0, "narrow": 0}
+    cases = []
+    while len(cases) < 3 * count_per_schedule:
+        m = rng.choice([rng.randint(1, 600), rng.randint(600, 5000), rng.randint(5000, 12000)])
+        n = rng.choice([rng.randint(1, 700), rng.randint(700, 8000), rng.randint(8000, 16000)])
+        sched = launch_plan("int8", m, n, 256)[0]
+        if counts[sched] >= count_per_schedule:
+            continue
+        counts[sched] += 1
+        k = 16 * rng.randint(1, 24)
+        cases.append((m, n, k, "bf16" if len(cases) % 3 == 2 else "int8", sched))
+    return cases
+
+
+def test_schedules_random_shapes_bit_identical(monkeypatch, device):
+    """60 seeded random shapes, 20 per schedule: the library's choice (plain, mixed or narrow)
+    gives the same bits as the plain launch, INT8 -> BF16 and BF16 -> BF16."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip("cases chosen for 256 CUs")
+    g = torch.Generator(device="cpu").manual_seed(11)
+    for m, n, k, mode, sched in _random_schedule_cases():
+        print(f"case m={m} n={n} k={k} {mode} {sched}", flush=True)
+        if mode == "int8":
+            a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
+            b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
+            kw = dict(a_scales=(torch.rand(m, generator=g) + 0.5).to(device),
+                      b_scales=(torch.rand(n, generator=g) + 0.5).to(device), output_dtype=torch.bfloat16)
+        else:
+            a = torch.randn((m, k), generator=g).to(torch.bfloat16).to(device)
+            b = torch.randn((n, k), generator=g).to(torch.bfloat16).to(device)
+            kw = dict(output_dtype=torch.bfloat16)
+        _set_schedule(monkeypatch, "auto")
+        auto = gemm(a, b, mode, **kw)
+        _set_schedule(monkeypatch, "plain")
+        plain = gemm(a, b, mode, **kw)
+        assert torch.equal(auto.view(torch.int16), plain.view(torch.int16)), (m, n, k, mode, sched)
+        del a, b, auto, plain
