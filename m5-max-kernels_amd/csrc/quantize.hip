@@ -16,7 +16,9 @@
 // prefetch, and a variant at 8 waves per SIMD, measured no faster.  Nor did four rows per
 // workgroup, unrolled so that each row's loads stay in flight across the previous row's
 // reduction (an LDS-only barrier, exact vmcnt waits): 40.6 us against 37.9 us for INT8, the
-// halved occupancy (118 VGPRs) costing more than the overlap gains.
+// halved occupancy (118 VGPRs) costing more than the overlap gains.  Giving each thread two
+// adjacent chunks, so that its codes leave in one 16-byte store, measured 10% slower for INT8
+// (4% faster for FP8).
 #include "m5k_common.h"
 
 namespace m5k {
