@@ -15,6 +15,10 @@ state: on MI355X the first ~100 steps after idle run 10-15% slower.  The headlin
 only a start and an end event around the K steps (per-step timing events add ~3%); a second
 pass of K steps with an event pair around each kernel gives the per-kernel durations that the
 roofline uses.
+
+--schedules prints instead one JSON line comparing, on the shapes of SCHEDULE_SHAPES, the GEMM
+schedule the library picks (mixed 256 x 256 + 256 x 128 tiles, or 256 x 224 tiles) with the
+plain launch: bit equality and ABBA-ordered device times.
 """
 
 from __future__ import annotations
@@ -422,6 +426,97 @@ def extras(torch, dev):
     return out
 
 
+# Shapes (mode, M, N, K) of the GEMM schedule comparison (--schedules): partial last rounds
+# that the library runs as mixed (256 x 256 + 256 x 128) or narrow (256 x 224) launches, and
+# the whole-round FFN-down shape that stays plain.
+SCHEDULE_SHAPES = [
+    ("int8", 9914, 4096, 4096), ("int8", 4096, 6144, 4096), ("int8", 4096, 5376, 5376),
+    ("int8", 4096, 14336, 5376), ("int8", 9914, 7168, 5376), ("int8", 4096, 7168, 5376),
+    ("int8", 2048, 5376, 5376), ("bf16", 4096, 5376, 5376), ("bf16", 4096, 7168, 5376),
+    ("int8", 4096, 4096, 16384),
+]
+
+
+def schedules_probe(torch, dev, rounds=6, reps=20):
+    """Each shape's library schedule against the plain launch (M5K_GEMM_MIXED_TILES=0 and
+    M5K_GEMM_NARROW_TILES=0), through the C ABI: bit equality, then ABBA rounds of `reps`
+    back-to-back calls between one event pair; medians."""
+    from m5kernels_amd import _lib
+    from m5kernels_amd.hip import launch_plan
+
+    off = {"M5K_GEMM_MIXED_TILES": "0", "M5K_GEMM_NARROW_TILES": "0"}
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = []
+    for mode, m, n, k in SCHEDULE_SHAPES:
+        if mode == "int8":
+            a = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
+            b = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+            sa = torch.rand(m, generator=g, device=dev) * 0.01 + 1e-3
+            sb = torch.rand(n, generator=g, device=dev) * 0.01 + 1e-3
+        else:
+            a = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+            b = torch.randn((n, k), generator=g, device=dev).to(torch.bfloat16)
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        st = _lib.stream_of(c)
+        if mode == "int8":
+            args = ("m5k_gemm_i8", _lib.ptr(a), _lib.ptr(b), m, n, k, _lib.ptr(sa), _lib.ptr(sb), _lib.ptr(c),
+                    _lib.BF16, None, None, None, None, None, st)
+        else:
+            args = ("m5k_gemm_float", _lib.ptr(a), _lib.ptr(b), _lib.BF16, m, n, k, _lib.ptr(c), _lib.BF16, None,
+                    None, None, st)
+
+        def run(plain):
+            saved = {v: os.environ.pop(v, None) for v in off}
+            if plain:
+                os.environ.update(off)
+            try:
+                _lib.call(*args)
+            finally:
+                for v, old in saved.items():
+                    if old is None:
+                        os.environ.pop(v, None)
+                    else:
+                        os.environ[v] = old
+
+        outs = []
+        for plain in (False, True):
+            c.fill_(7.0)
+            run(plain)
+            torch.cuda.synchronize()
+            outs.append(c.clone())
+        same = bool(torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)))
+        # ~50 ms of load first: the clocks settle to their sustained state (as in the headline run).
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 0.05:
+            for _ in range(20):
+                run(False)
+            torch.cuda.synchronize()
+        times = {False: [], True: []}
+        for r in range(rounds):
+            for plain in ((False, True) if r % 2 == 0 else (True, False)):
+                for _ in range(5):
+                    run(plain)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                torch.cuda._sleep(20_000_000)
+                e0.record()
+                for _ in range(reps):
+                    run(plain)
+                e1.record()
+                torch.cuda.synchronize()
+                times[plain].append(e0.elapsed_time(e1) / reps)
+        sched_ms, plain_ms = statistics.median(times[False]), statistics.median(times[True])
+        plan, full = launch_plan(mode, m, n, cus)
+        out.append({"mode": mode, "m": m, "n": n, "k": k, "schedule": plan, "mixed_full_tiles": full,
+                    "schedule_ms": sched_ms, "plain_ms": plain_ms, "speedup": plain_ms / sched_ms,
+                    "bit_identical": same})
+        log(f"[bench] schedules {mode} {m}x{n}x{k}: {plan} {sched_ms * 1e3:.1f} us, plain {plain_ms * 1e3:.1f} us, "
+            f"x{plain_ms / sched_ms:.3f}, bit-identical {same}")
+        del a, b, c, outs
+    return out
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
@@ -433,6 +528,8 @@ def main():
     p.add_argument("--no-extras", action="store_true", help="skip the other configurations (profiling runs)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a 256 MiB device copy x5 (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--schedules", action="store_true",
+                   help="only compare the library's GEMM schedules (mixed / narrow) with the plain launch")
     args = p.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -456,6 +553,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log("[bench] copied 256 MiB x5")
+        return
+    if args.schedules:
+        res = schedules_probe(torch, dev)
+        print(json.dumps({"schedules": res}))
+        if not all(r["bit_identical"] for r in res):
+            sys.exit(1)
         return
     log(f"[bench] inputs: A bf16 [{M},{K}], W bf16 [{N},{K}], seed {SEED}")
     a, w = make_inputs(torch, dev)
