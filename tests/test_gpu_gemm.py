@@ -466,14 +466,16 @@ def _random_schedule_cases(count_per_schedule=20, seed=2024):
         if counts[sched] >= count_per_schedule:
             continue
         counts[sched] += 1
-        k = 16 * rng.randint(1, 24)
-        cases.append((m, n, k, "bf16" if len(cases) % 3 == 2 else "int8", sched))
+        mode = ("int8", "bf16", "fp16", "fp32", "fp8")[len(cases) % 5]
+        k = 128 * rng.randint(1, 3) if mode == "fp8" else 16 * rng.randint(1, 24)
+        cases.append((m, n, k, mode, sched))
     return cases
 
 
 def test_schedules_random_shapes_bit_identical(monkeypatch, device):
-    """60 seeded random shapes, 20 per schedule: the library's choice (plain, mixed or narrow)
-    gives the same bits as the plain launch, INT8 -> BF16 and BF16 -> BF16."""
+    """60 seeded random shapes, 20 per INT8 schedule, spread over the five modes: the library's
+    choice (plain, mixed, or narrow for the 16 x 16 modes) gives the same bits as the plain
+    launch."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if cus != 256:
         pytest.skip("cases chosen for 256 CUs")
@@ -485,13 +487,19 @@ def test_schedules_random_shapes_bit_identical(monkeypatch, device):
             b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
             kw = dict(a_scales=(torch.rand(m, generator=g) + 0.5).to(device),
                       b_scales=(torch.rand(n, generator=g) + 0.5).to(device), output_dtype=torch.bfloat16)
+        elif mode == "fp8":
+            a, sa = quantize(torch.randn((m, k), generator=g).to(torch.bfloat16).to(device), "fp8")
+            b, sb = quantize(torch.randn((n, k), generator=g).to(torch.bfloat16).to(device), "fp8")
+            kw = dict(a_scales=sa, b_scales=sb, output_dtype=torch.float32)
         else:
-            a = torch.randn((m, k), generator=g).to(torch.bfloat16).to(device)
-            b = torch.randn((n, k), generator=g).to(torch.bfloat16).to(device)
-            kw = dict(output_dtype=torch.bfloat16)
+            dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[mode]
+            a = torch.randn((m, k), generator=g).to(dt).to(device)
+            b = torch.randn((n, k), generator=g).to(dt).to(device)
+            kw = dict(output_dtype=dt)
         _set_schedule(monkeypatch, "auto")
         auto = gemm(a, b, mode, **kw)
         _set_schedule(monkeypatch, "plain")
         plain = gemm(a, b, mode, **kw)
-        assert torch.equal(auto.view(torch.int16), plain.view(torch.int16)), (m, n, k, mode, sched)
+        view = torch.int16 if auto.element_size() == 2 else torch.int32
+        assert torch.equal(auto.view(view), plain.view(view)), (m, n, k, mode, sched)
         del a, b, auto, plain
