@@ -141,9 +141,10 @@ __global__ __launch_bounds__(G::THREADS, 1) void gemm_kernel(const uint8_t* __re
 // into two 256 x 128 halves, which take a little over half a tile's time each, so the leftover
 // work runs as one shorter, better-filled round.  Each output element is still one
 // workgroup's dot product over all of K: results are bit-identical to the plain launch.
-// Workgroups [0, full) are the full tiles; workgroup full + h is half h & 1 of tile
-// full + h / 2 (full is a multiple of 8, so both parts keep the XCD-contiguous numbering of
-// tile_coords and the two halves of a tile land on one XCD).
+// Workgroups [0, full) are the full tiles.  Workgroup full + w runs logical half
+// h = xcd_logical(w), which is half h & 1 of tile full + h / 2 in the raster order.  full is
+// a multiple of 8, so w keeps the hardware's XCD (w % 8 == (full + w) % 8), each XCD gets a
+// contiguous run of h, and the two halves of a tile land on one XCD.
 using HalfGrid = Grid8Half;
 
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
