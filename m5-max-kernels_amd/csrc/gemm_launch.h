@@ -144,7 +144,8 @@ __global__ __launch_bounds__(G::THREADS, 1) void gemm_kernel(const uint8_t* __re
 // Workgroups [0, full) are the full tiles.  Workgroup full + w runs logical half
 // h = xcd_logical(w), which is half h & 1 of tile full + h / 2 in the raster order.  full is
 // a multiple of 8, so w keeps the hardware's XCD (w % 8 == (full + w) % 8), each XCD gets a
-// contiguous run of h, and the two halves of a tile land on one XCD.
+// contiguous run of h, and the two halves of a tile land on one XCD unless a run boundary
+// falls between them.
 using HalfGrid = Grid8Half;
 
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW>
