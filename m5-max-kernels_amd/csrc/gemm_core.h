@@ -72,6 +72,7 @@ using Grid4 = Grid<2, 2>;
 using Grid8 = Grid<2, 4>;
 using Grid8Half = Grid<4, 2, BN / 2>;     // 256 x 128 tile, 8 waves of 64 x 64
 using Grid8Narrow = Grid<4, 2, 7 * BN / 8>;  // 256 x 224 tile, 8 waves of 64 x 112 (16 x 16 modes)
+using Grid8Skinny = Grid<8, 1, BN / 4>;      // 256 x 64 tile, 8 waves of 32 x 64 (split-K of short M)
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <int MODE>

@@ -88,16 +88,24 @@ def _check_vector(t, n, dtype, message):
         raise ValueError(message)
 
 
-def splitk_plan(m, n, k):
+def splitk_plan(m, n, k, cus=256):
     """Number of K ranges per output tile for the W8A8 linear (1 = one workgroup per tile).
 
     Shapes with few 256 x 256 tiles (short M) leave most of the 256 CUs idle; splitting K
     aims at ~224 workgroups, each over at least 4 slabs of 64 bytes.  The INT32 partial
     tiles cost 8 * splits * M * N bytes of extra traffic against the N * K bytes of weights,
     so splits also stay below K / (2 M).  (Measured on MI355X over M 16..512 and H3 widths:
-    within ~10% of the best split count, 1.4-3.7x faster than one workgroup per tile.)"""
-    tiles = -(-m // 256) * -(-n // 256)
+    within ~10% of the best split count, 1.4-3.7x faster than one workgroup per tile.)
+
+    One tile row (M <= 256) with K <= 8192 first tries the library's 256 x 64 split tiles,
+    which m5k_gemm_i8_splitk uses whenever ceil(N / 64) * splits fits in one round of `cus`
+    workgroups: fewer K ranges then fill the chip (measured 1.4-1.6x faster at K 4096-5376)."""
     slabs = -(-k // 64)
+    if m <= 256 and k <= 8192:
+        splits = min(cus // -(-n // 64), slabs // 4, max(2, k // (2 * m)), 64)
+        if splits >= 2:
+            return splits
+    tiles = -(-m // 256) * -(-n // 256)
     splits = min(224 // tiles, slabs // 4, max(2, k // (2 * m)), 64)
     return splits if splits >= 2 else 1
 
@@ -264,7 +272,7 @@ def gemm(
             bias = _lib.device_tensor(bias, "bias")
             bias_row_map = None if bias_row_map is None else _lib.device_tensor(bias_row_map, "bias_row_map")
         aligned = k % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
-        splits = splitk_plan(m, n, k) if aligned else 1
+        splits = splitk_plan(m, n, k, _cu_count(a.device)) if aligned else 1
         # The library's mixed and narrow launches refill a partial last round without INT32
         # partials and measured faster wherever both apply; the split-K tail takes the rest.
         cus = _cu_count(a.device) if aligned and splits == 1 else 0
