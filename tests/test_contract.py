@@ -261,8 +261,12 @@ def test_tail_split_plan_decisions():
     # One tile row, K <= 8192: split counts sized to 256 x 64 tiles (64 columns at N 4096).
     assert splitk_plan(128, 4096, 4096) == 4 and splitk_plan(1, 4096, 4096) == 4
     assert splitk_plan(128, 7168, 5376) == 2 and splitk_plan(128, 1536, 5376) == 10
-    # 224 narrow columns need two rounds even at 2 splits, and K > 8192 keeps 256 x 256 tiles.
-    assert splitk_plan(128, 14336, 5376) == 4 and splitk_plan(128, 5376, 14336) == 10
+    # 224 columns of 64 need two rounds even at 2 splits: 256 x 128 tiles (112 columns) take
+    # them, and K > 8192 goes straight to 256 x 128 tiles.
+    assert splitk_plan(128, 14336, 5376) == 2 and splitk_plan(128, 5376, 14336) == 6
+    assert splitk_plan(128, 4096, 16384) == 8
+    # 448 columns of 128 still need two rounds: 256 x 256 tiles with the general rule.
+    assert splitk_plan(128, 28672, 5376) == 2
     for m in range(256, 12000, 397):
         for n in (1536, 4096, 5120, 5376, 7168):
             plan = tail_split_plan(m, n, 4096)
