@@ -115,8 +115,8 @@ int m5k_gemm_i8(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t 
                 void* stream);
 
 /*
- * The same W8A8 linear as m5k_gemm_i8 for short M: each output tile (256 x 256; for m <= 256,
- * 256 x 64 (k <= 8192) or 256 x 128 when ceil(n/width) * splits fits in one round) is split over `splits`
+ * The same W8A8 linear as m5k_gemm_i8 for short M: each output tile (256 x 256, or 256 x 64
+ * (k <= 8192) or 256 x 128 when the tiles x splits fit in one round) is split over `splits`
  * contiguous ranges of K (1..64), the raw INT32 partial tiles go to workspace[splits][m][n]
  * (int32, caller-owned, at least splits*m*n elements), and a second kernel sums them in
  * split order and applies the identical epilogue.  INT32 sums are exact, so c is bit-identical

@@ -352,15 +352,15 @@ int launch_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_
   const int64_t kt_total = k_stages(k);
   const int64_t per = (kt_total + splits - 1) / splits;
   const int used = static_cast<int>((kt_total + per - 1) / per);  // no empty split
-  // One tile row (M <= 256): 256 x 64 tiles (K <= 8192) or 256 x 128 tiles when their
-  // workgroups fit in one round, so a few K ranges fill the chip and the INT32 partials
-  // (splits x M x N) stay small next to the weights streamed.  Measured against 256 x 256
-  // tiles with the split count sized to each: 256 x 64 1.4-1.6x faster at K 4096-5376 (M 1-256),
-  // equal at K 16384 and 5% slower at K 14336, hence its K limit; 256 x 128 1.15-1.23x faster
-  // where 256 x 64 does not fit (N 14336, or K 14336-16384).
+  // 256 x 64 tiles (K <= 8192) or 256 x 128 tiles when their workgroups fit in one round, so
+  // a few K ranges fill the chip and the INT32 partials (splits x M x N) stay small next to the
+  // weights streamed.  Measured against 256 x 256 tiles with the split count sized to each:
+  // 256 x 64 1.4-1.6x faster at K 4096-5376 (M 1-256), equal at K 16384 and 5% slower at K
+  // 14336, hence its K limit; 256 x 128 1.15-1.23x faster where 256 x 64 does not fit (N 14336,
+  // or K 14336-16384); at M 384-1024 the narrower tiles were 1.1-1.45x faster.
   const int cus = device_cus();
   auto fits = [&](int width) {
-    return m <= BM && cus > 0 && ((n + width - 1) / width) * used <= static_cast<int64_t>(cus);
+    return cus > 0 && ((m + BM - 1) / BM) * ((n + width - 1) / width) * used <= static_cast<int64_t>(cus);
   };
   const int tn = k <= 8192 && fits(Grid8Skinny::TN) ? Grid8Skinny::TN : fits(HalfGrid::TN) ? HalfGrid::TN : BN;
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + tn - 1) / tn);

@@ -97,18 +97,22 @@ def splitk_plan(m, n, k, cus=256):
     so splits also stay below K / (2 M).  (Measured on MI355X over M 16..512 and H3 widths:
     within ~10% of the best split count, 1.4-3.7x faster than one workgroup per tile.)
 
-    One tile row (M <= 256) first tries the library's narrower split tiles, which
-    m5k_gemm_i8_splitk uses whenever ceil(N / width) * splits fits in one round of `cus`
-    workgroups: 256 x 64 (K <= 8192), then 256 x 128.  Fewer K ranges then fill the chip
-    (measured 1.4-1.6x faster at K 4096-5376 with 64-wide tiles, 1.15-1.23x at N 14336 or
-    K 14336-16384 with 128-wide ones)."""
+    It first tries the library's narrower split tiles, which m5k_gemm_i8_splitk uses whenever
+    ceil(M / 256) * ceil(N / width) * splits fits in one round of `cus` workgroups: 256 x 64
+    (K <= 8192), then 256 x 128.  Fewer K ranges then fill the chip (measured 1.4-1.6x faster
+    at K 4096-5376 with 64-wide tiles, 1.15-1.23x at N 14336 or K 14336-16384 with 128-wide
+    ones, 1.1-1.45x at M 384-1024).  Above M = 768 the plain launch, with the library's
+    mixed or narrow tiles, measured faster than any split (M 1024: 44.8 against 57.6 us at
+    N = K = 5376, 35.5 against 37.2 us at N = K = 4096), so no split is planned there."""
+    if m > 768:
+        return 1
     slabs = -(-k // 64)
-    if m <= 256:
-        for width in ((64, 128) if k <= 8192 else (128,)):
-            splits = min(cus // -(-n // width), slabs // 4, max(2, k // (2 * m)), 64)
-            if splits >= 2:
-                return splits
-    tiles = -(-m // 256) * -(-n // 256)
+    tiles_m = -(-m // 256)
+    for width in ((64, 128) if k <= 8192 else (128,)):
+        splits = min(cus // (tiles_m * -(-n // width)), slabs // 4, max(2, k // (2 * m)), 64)
+        if splits >= 2:
+            return splits
+    tiles = tiles_m * -(-n // 256)
     splits = min(224 // tiles, slabs // 4, max(2, k // (2 * m)), 64)
     return splits if splits >= 2 else 1
 
