@@ -101,10 +101,11 @@ def splitk_plan(m, n, k, cus=256):
     ceil(M / 256) * ceil(N / width) * splits fits in one round of `cus` workgroups: 256 x 64
     (K <= 8192), then 256 x 128.  Fewer K ranges then fill the chip (measured 1.4-1.6x faster
     at K 4096-5376 with 64-wide tiles, 1.15-1.23x at N 14336 or K 14336-16384 with 128-wide
-    ones, 1.1-1.45x at M 384-1024).  Above M = 768 the plain launch, with the library's
-    mixed or narrow tiles, measured faster than any split (M 1024: 44.8 against 57.6 us at
-    N = K = 5376, 35.5 against 37.2 us at N = K = 4096), so no split is planned there."""
-    if m > 768:
+    ones, 1.1-1.45x at M 384-1024).  Above M = 768, with at least 32 tiles of 256 x 256, the
+    plain launch (the library's mixed or narrow tiles) measured faster than any split (M 1024:
+    44.8 against 57.6 us at N = K = 5376, 35.5 against 37.2 us at N = K = 4096), so no split is
+    planned there; narrow outputs (N 32-96) keep the split, their few tiles leaving most CUs idle."""
+    if m > 768 and -(-m // 256) * -(-n // 256) >= 32:
         return 1
     slabs = -(-k // 64)
     tiles_m = -(-m // 256)

@@ -257,8 +257,10 @@ def test_tail_split_plan_decisions():
     for shape in [(9914, 4096, 4096), (4096, 5376, 2048), (4096, 14336, 5376), (4096, 7168, 5376),
                   (4096, 4096, 16384), (1024, 5376, 5376)]:
         assert tail_split_plan(*shape) is None, shape
-    # Above M = 768 the plain launch (mixed / narrow tiles) measured faster than any split.
+    # Above M = 768 the plain launch (mixed / narrow tiles) measured faster than any split,
+    # except for narrow outputs whose few tiles leave most CUs idle.
     assert splitk_plan(1024, 5376, 5376) == 1 and splitk_plan(1024, 4096, 4096) == 1
+    assert splitk_plan(1024, 96, 5376) == 2 and splitk_plan(1024, 32, 5376) == 2
     # Two tile rows: 256 x 64 split tiles while 2 * ceil(N / 64) * splits fits one round.
     assert splitk_plan(512, 4096, 4096) == 2 and splitk_plan(512, 1536, 5376) == 5
     # One tile row, K <= 8192: split counts sized to 256 x 64 tiles (64 columns at N 4096).
