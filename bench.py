@@ -10,8 +10,9 @@ Prints ONE JSON line: value = TOPS = 2*M*N*K / (ms per online step), the rooflin
 dominant kernel (the GEMM, dense INT8 MFMA peak), per-kernel HIP-event timings and the CPU
 baseline (the oracle's C/OpenMP W8A8 on a bounded row sample, rank 0 only).
 
-Timing.  The default warmup (200 steps, ~50 ms of load) brings the device to its steady clock
-state: on MI355X the first ~100 steps after idle run 10-15% slower.  The headline region has
+Timing.  After the W warmup steps, further untimed steps run until at least --settle-seconds
+(0.4 s) of device time has passed, whatever W is: on MI355X the first ~100 steps after idle run
+10-15% slower while the clocks ramp (the count is reported as settle_steps).  The headline region has
 only a start and an end event around the K steps (per-step timing events add ~3%); a second
 pass of K steps with an event pair around each kernel gives the per-kernel durations that the
 roofline uses.
@@ -517,6 +518,69 @@ def schedules_probe(torch, dev, rounds=6, reps=20):
     return out
 
 
+def settle(torch, fn, seconds):
+    """Run fn back to back for at least `seconds` of device time (synchronizing every 10 calls):
+    MI355X ramps its clocks over the first ~100 ms of sustained MFMA load after idle."""
+    t0, calls = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        calls += 10
+        torch.cuda.synchronize()
+    return calls
+
+
+def counter_workload(torch, dev, reps):
+    """The kernels whose hardware counters the profiles quote, `reps` launches each after a
+    clock-settling run, in this order: the FFN-down INT8 GEMM (ours), hipBLASLt's INT8 GEMM
+    (torch._int_mm) on the same codes, the FFN-down FP8 GEMM, the INT8 and FP8 quantizers on
+    the FFN-down activation, the fused gated and ungated prep (M 4096, K 4096, H128) and the
+    RMS quantizer (M 4096, K 4096, H256).  For rocprofv3 --pmc runs; prints nothing else."""
+    from m5kernels_amd import (fused_gated_residual_norm_hadamard_quantize, fused_norm_hadamard_quantize, gemm,
+                               quantize, rms_quantize)
+
+    a, w = make_inputs(torch, dev)
+    wq, ws = quantize(w, "int8")
+    aq, sa = quantize(a, "int8")
+    w8, ws8 = quantize(w, "fp8")
+    a8, sa8 = quantize(a, "fp8")
+    wq_t = wq.t()
+    bf = torch.bfloat16
+    ours = lambda: gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=bf)  # noqa: E731
+    settle(torch, ours, 0.3)
+    runs = [
+        ("gemm_i8", ours),
+        ("hipblaslt_int_mm", lambda: torch._int_mm(aq, wq_t)),
+        ("gemm_f8", lambda: gemm(a8, w8, "fp8", a_scales=sa8, b_scales=ws8, output_dtype=bf)),
+        ("quantize_int8", lambda: quantize(a, "int8")),
+        ("quantize_fp8", lambda: quantize(a, "fp8")),
+    ]
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    m, k, tables = 4096, 4096, 2
+    res = torch.randn((m, k), generator=g, device=dev).to(bf)
+    branch = torch.randn((m, k), generator=g, device=dev).to(bf)
+    gate, scale, shift = ((torch.randn((tables, k), generator=g, device=dev) * 0.1).to(bf) for _ in range(3))
+    gamma = (1 + 0.1 * torch.randn((k,), generator=g, device=dev)).to(bf)
+    row_map = (torch.arange(m, device=dev, dtype=torch.int32) * tables // m).to(torch.int32)
+    signs = torch.ones(k, dtype=torch.int8, device=dev)
+    kw = dict(norm="layer", epsilon=1e-5, round_output="input", row_map=row_map)
+    gamma32 = gamma.float()
+    runs += [
+        ("prep_gated", lambda: fused_gated_residual_norm_hadamard_quantize(
+            res, branch, gate, gamma, scale, shift, signs, 128, gate_row_map=row_map, **kw)),
+        ("prep_ungated", lambda: fused_norm_hadamard_quantize(res, gamma, scale, shift, signs, 128, **kw)),
+        ("rms_quantize", lambda: rms_quantize(res, gamma32, signs, 256)),
+    ]
+    for name, fn in runs:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        log(f"[bench] counter workload: {name} x{reps}")
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
@@ -530,6 +594,10 @@ def main():
                    help="only run a 256 MiB device copy x5 (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     p.add_argument("--schedules", action="store_true",
                    help="only compare the library's GEMM schedules (mixed / narrow) with the plain launch")
+    p.add_argument("--counter-workload", type=int, default=0, metavar="REPS",
+                   help="only launch each profiled kernel REPS times (for rocprofv3 --pmc runs)")
+    p.add_argument("--settle-seconds", type=float, default=0.4,
+                   help="minimum device time of the warmup, whatever --warmup says (clock ramp)")
     args = p.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -554,6 +622,9 @@ def main():
         torch.cuda.synchronize()
         log("[bench] copied 256 MiB x5")
         return
+    if args.counter_workload:
+        counter_workload(torch, dev, args.counter_workload)
+        return
     if args.schedules:
         res = schedules_probe(torch, dev)
         print(json.dumps({"schedules": res}))
@@ -569,9 +640,12 @@ def main():
         aq, sa = quantize(a, "int8")
         return gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
 
-    log(f"[bench] warmup {args.warmup}")
+    log(f"[bench] warmup {args.warmup} steps, then at least {args.settle_seconds} s of steps")
     for _ in range(args.warmup):
         y = step()
+    torch.cuda.synchronize()
+    settle_steps = settle(torch, step, args.settle_seconds)
+    y = step()
     torch.cuda.synchronize()
 
     steps = args.steps
@@ -630,6 +704,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
+        "settle_steps": settle_steps,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",

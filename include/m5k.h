@@ -197,8 +197,10 @@ int m5k_hadamard_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t
  * fused_gated_residual_norm_hadamard_quantize (src/m5kernels/norm_hadamard.py:122-265,
  * shaders/norm_hadamard.metal:1-121).
  *   x: [rows,k] of x_dtype (the residual when gated); k % block == 0.
- *   gated: branch [rows,k] (x_dtype), gate [k] or [P,k] with gate_row_map[rows];
+ *   gated: branch [rows,k] of branch_dtype (x_dtype, or F32 for a branch of another float
+ *          dtype, widened exactly by the caller), gate [k] or [P,k] with gate_row_map[rows];
  *          residual_out[rows,k] (x_dtype) receives R(x + branch*gate), written once.
+ *          branch_dtype is ignored when branch is NULL.
  *   gamma [k]; scale/shift [k], or [P,k] tables selected by row_map[rows]; gamma, scale,
  *   shift and gate share param_dtype (BF16 or F32).  signs int8 [k].
  *   norm: M5K_NORM_RMS / M5K_NORM_LAYER; round_to_input: 1 rounds the modulated value to
@@ -206,7 +208,8 @@ int m5k_hadamard_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t
  *   Outputs: q int8 [rows,k], scales float32 [rows].
  */
 int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t rows, int64_t k, const void* branch,
-                               const void* gate, const int32_t* gate_row_map, const void* gamma,
+                               int branch_dtype, const void* gate, const int32_t* gate_row_map,
+                               const void* gamma,
                                const void* scale, const void* shift, int param_dtype,
                                const int32_t* row_map, const int8_t* signs, int block, int norm,
                                float epsilon, int round_to_input, int8_t* q, float* scales,
@@ -224,11 +227,12 @@ int m5k_norm_modulate(const void* x, int x_dtype, int64_t rows, int64_t k, const
 /*
  * Staged gated residual update out = R(float(residual) + float(branch) * float(gate)).
  * Replaces norm_hadamard.gated_residual_add (src/m5kernels/norm_hadamard.py:280-300,
- * shaders/gated_residual.metal:1-9).  gate [k] or [P,k] with gate_row_map[rows].
+ * shaders/gated_residual.metal:1-9).  gate [k] or [P,k] with gate_row_map[rows]; branch of
+ * branch_dtype: the residual dtype, or F32 for a branch of another float dtype.
  */
 int m5k_gated_residual_add(const void* residual, int dtype, int64_t rows, int64_t k, const void* branch,
-                           const void* gate, int gate_dtype, const int32_t* gate_row_map, void* out,
-                           void* stream);
+                           int branch_dtype, const void* gate, int gate_dtype, const int32_t* gate_row_map,
+                           void* out, void* stream);
 
 /*
  * Q or K projection + per-head RMSNorm + split-half RoPE, head-major BF16 output.

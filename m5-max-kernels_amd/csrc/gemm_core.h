@@ -205,6 +205,12 @@ __device__ __forceinline__ v4i buffer_rsrc(const void* base, uint32_t num_record
              static_cast<int>(num_records), 0x00020000};
 }
 
+// Wave-uniform buffer window [base + ofs, base + records): the descriptor of one K stage of a
+// tile's rows (scalar arithmetic only; ofs <= records).
+__device__ __forceinline__ v4i window_rsrc(const uint8_t* base, uint32_t records, uint32_t ofs) {
+  return buffer_rsrc(base + ofs, records - ofs);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(const_cast<void*>(p))));
 }
@@ -356,7 +362,8 @@ __device__ __forceinline__ void mfma_rows_reading(AccTile<MODE, G>& acc, const F
 // Number of 128-byte K stages of a row of Kb bytes.
 __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 1) / BKB; }
 
-// Direct-to-LDS main loop (rows 16-byte multiples, bases 16-byte aligned, operands < 2 GiB).
+// Direct-to-LDS main loop (rows 16-byte multiples of at most 2^23 bytes, bases 16-byte aligned;
+// operands of any size, each workgroup addressing only its own rows).
 //
 // DMA: per stage each wave moves DMA_ROWS rows of both operand tiles with DMA_INSTR + DMA_INSTR
 // buffer loads of 1 KiB: lane l -> row 8i + l/8, physical chunk l & 7, i.e. whole 128-byte
@@ -389,13 +396,18 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
   zero_acc<MODE, G>(acc);
 
-  const v4i rsrc_a = buffer_rsrc(A, static_cast<uint32_t>((int64_t)M * Kb));
-  const v4i rsrc_b = buffer_rsrc(B, static_cast<uint32_t>((int64_t)N * Kb));
+  // Each workgroup addresses only its own rows: the windows [A + tile_m0 * Kb, + rows_a * Kb)
+  // and [B + tile_n0 * Kb, + rows_b * Kb) are at most 256 rows of Kb < 2^23 bytes, so 32-bit
+  // buffer offsets cover operands of any size.
   constexpr uint32_t kOob = 0x80000000u;  // beyond num_records: the load returns zeros
   const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform copy for LDS bases
+  const int rows_a = min(M - tile_m0, BM), rows_b = min(N - tile_n0, G::TN);
+  const uint8_t* a_win = A + static_cast<int64_t>(tile_m0) * Kb;
+  const uint8_t* b_win = B + static_cast<int64_t>(tile_n0) * Kb;
+  const uint32_t rec_a = static_cast<uint32_t>(rows_a * Kb), rec_b = static_cast<uint32_t>(rows_b * Kb);
 
-  // Per-lane source offsets of each DMA instruction (kOob for rows past M / N) and the byte
-  // offset of the logical chunk the lane moves.  Instruction i covers rows
+  // Per-lane window offsets of each DMA instruction (kOob for rows past the window) and the
+  // byte offset of the logical chunk the lane moves.  Instruction i covers rows
   // wave * DMA_ROWS + 8i + [0, 8) (DMA_ROWS a multiple of 16), whose swizzle is
   // 4 (i & 1) + (l >> 4): the chunk offset depends on the parity of i only.
   static_assert(G::DMA_ROWS % 16 == 0 && G::DMA_ROWS_B % 16 == 0, "DMA row groups start at even row pairs");
@@ -405,26 +417,33 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
 #pragma unroll
   for (int i = 0; i < G::DMA_INSTR; ++i) {
     const int r = wave * G::DMA_ROWS + 8 * i + (lane >> 3);
-    a_base[i] = tile_m0 + r < M ? static_cast<uint32_t>((int64_t)(tile_m0 + r) * Kb) + lchunk[i & 1] : kOob;
+    a_base[i] = r < rows_a ? static_cast<uint32_t>(r * Kb) + lchunk[i & 1] : kOob;
   }
 #pragma unroll
   for (int i = 0; i < G::DMA_INSTR_B; ++i) {
     const int r = wave * G::DMA_ROWS_B + 8 * i + (lane >> 3);
-    b_base[i] = r < G::TN && tile_n0 + r < N ? static_cast<uint32_t>((int64_t)(tile_n0 + r) * Kb) + lchunk[i & 1]
-                                             : kOob;
+    b_base[i] = r < rows_b ? static_cast<uint32_t>(r * Kb) + lchunk[i & 1] : kOob;
   }
   const uint32_t lds_row0 = static_cast<uint32_t>(uwave * G::DMA_ROWS * BKB);
   const uint32_t lds_row0_b = static_cast<uint32_t>(uwave * G::DMA_ROWS_B * BKB);
-  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {  // kr: stage index relative to kt_begin
+  // Stage kr (relative to kt_begin) moves the window start by the stage offset (scalar) and
+  // keeps the lane offsets: row r's chunk then ends before row r + 1 starts, and rows past the
+  // window stay out of range.  In the last partial stage of a ragged K (Kb % 128 != 0) the lanes
+  // whose chunk starts at or past K set the offset's top bit (out of range: zeros); stages past
+  // the range use an empty window.  One VALU op per DMA instruction.
+  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {
     const uint32_t kofs = static_cast<uint32_t>((kt_begin + kr) * BKB);
-    const bool live = kr < kt_count;
     const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0_b;
+    const bool live = kr < kt_count;
+    const int64_t rem = Kb - static_cast<int64_t>(kofs);  // bytes of K left at this stage
+    const uint32_t kill[2] = {static_cast<int64_t>(lchunk[0]) < rem ? 0u : kOob,
+                              static_cast<int64_t>(lchunk[1]) < rem ? 0u : kOob};
+    const uint32_t ofs = live ? kofs : 0;
+    const v4i ra = window_rsrc(a_win, live ? rec_a : 0, ofs), rb = window_rsrc(b_win, live ? rec_b : 0, ofs);
 #pragma unroll
     for (int i = 0; i < G::DMA_INSTR; ++i) {
-      const bool kin = live && static_cast<int64_t>(kofs) + lchunk[i & 1] < Kb;
-      dma16(la + 8 * i * BKB, (kin && a_base[i] != kOob) ? a_base[i] + kofs : kOob, rsrc_a);
-      if (i < G::DMA_INSTR_B)
-        dma16(lb + 8 * i * BKB, (kin && b_base[i] != kOob) ? b_base[i] + kofs : kOob, rsrc_b);
+      dma16(la + 8 * i * BKB, a_base[i] | kill[i & 1], ra);
+      if (i < G::DMA_INSTR_B) dma16(lb + 8 * i * BKB, b_base[i] | kill[i & 1], rb);
     }
   };
 

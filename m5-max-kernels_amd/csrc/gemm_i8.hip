@@ -73,8 +73,7 @@ extern "C" int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, i
   M5K_REQUIRE(!(bias && residual), "%s: bias and gated residual cannot be combined", name);
   M5K_REQUIRE(!residual || c_dtype == M5K_BF16, "%s: gated epilogue requires BF16 output", name);
   M5K_REQUIRE(splits >= 1 && splits <= 64, "%s: splits=%d outside [1,64]", name, splits);
-  M5K_REQUIRE(k % 16 == 0 && aligned16(a) && aligned16(b) && m * k < (int64_t(1) << 31) && n * k < (int64_t(1) << 31),
-              "%s: split-K needs 16-byte aligned operands with K %% 16 == 0 and operands under 2 GiB", name);
+  M5K_REQUIRE(dma_ok(a, b, k), "%s: split-K needs 16-byte aligned operands with K %% 16 == 0", name);
   M5K_REQUIRE(workspace_elems >= static_cast<int64_t>(splits) * m * n, "%s: workspace holds %lld INT32, needs %lld",
               name, (long long)workspace_elems, (long long)(static_cast<int64_t>(splits) * m * n));
   EpiParams p{a_scales, b_scales, c, bias, bias_row_map, static_cast<const uint16_t*>(residual),

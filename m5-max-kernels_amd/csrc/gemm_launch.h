@@ -11,6 +11,7 @@
 #pragma once
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 
 #include "gemm_core.h"
 
@@ -240,11 +241,37 @@ inline bool narrow_pays(int64_t m, int64_t n, int cus, int64_t mixed_full) {
   return narrow < 0.95 * other;
 }
 
+// The direct-to-LDS main loop needs 16-byte aligned rows and bases and 256-row windows that
+// fit a 32-bit buffer offset (rows of at most 2^23 bytes); other operands take the
+// register-staged loop.
+inline bool dma_ok(const void* a, const void* b, int64_t kb) {
+  return kb % 16 == 0 && kb <= (int64_t(1) << 23) && aligned16(a) && aligned16(b);
+}
+
 enum Schedule { SCHED_PLAIN = 0, SCHED_MIXED = 1, SCHED_NARROW = 2 };
+
+// A schedule named by M5K_GEMM_SCHEDULE ("plain", "mixed", "narrow"; read on every call, for
+// tuners that measure each one), or -1.  A forced mixed launch keeps the planner's full-tile
+// count when it has one, else runs every tile of the last (or only) round as two halves.
+inline int forced_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& full) {
+  const char* env = std::getenv("M5K_GEMM_SCHEDULE");
+  if (env == nullptr || env[0] == '\0') return -1;
+  full = -1;
+  if (std::strcmp(env, "plain") == 0) return SCHED_PLAIN;
+  if (std::strcmp(env, "narrow") == 0) return md16 ? SCHED_NARROW : SCHED_PLAIN;
+  if (std::strcmp(env, "mixed") == 0 && cus >= XCDS && cus % XCDS == 0) {
+    const int64_t total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    full = mixed_full_tiles(m, n, cus);
+    if (full < 0) full = total > cus ? (total - 1) / cus * cus : 0;
+    return SCHED_MIXED;
+  }
+  return -1;
+}
 
 // Launch schedule of an aligned GEMM with an [m, n] output on `cus` CUs; `full` receives the
 // mixed launch's full tiles (-1 otherwise).  Narrow tiles exist for the 16 x 16 modes only.
 inline int plan_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& full) {
+  if (const int forced = forced_schedule(md16, m, n, cus, full); forced >= 0) return forced;
   full = mixed_full_tiles(m, n, cus);
   if (md16 && narrow_pays(m, n, cus, full)) {
     full = -1;
@@ -259,9 +286,8 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   const int64_t kb = k * Traits<MODE>::elem_bytes;
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
   M5K_REQUIRE(tiles <= 0x7FFFFFFF, "%s: too many tiles", name);
-  // The direct-to-LDS path addresses each operand through a 32-bit buffer descriptor.
-  const bool aligned = kb % 16 == 0 && aligned16(a) && aligned16(b) && m * kb < (int64_t(1) << 31) &&
-                       n * kb < (int64_t(1) << 31);
+  // The direct-to-LDS path addresses a tile's rows through 32-bit buffer windows.
+  const bool aligned = dma_ok(a, b, kb);
   const dim3 grid(static_cast<unsigned>(tiles)), block(KernelGrid::THREADS);
   auto* A = static_cast<const uint8_t*>(a);
   auto* B = static_cast<const uint8_t*>(b);

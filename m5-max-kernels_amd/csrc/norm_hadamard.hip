@@ -96,14 +96,14 @@ struct GroupRow {  // one workgroup of 4 wave64 per row
 
 // Row input for 8 elements at column j: X, or the gated residual update rounded to the
 // residual dtype and written to R_next (FP32 product, then add, then one cast).
-template <int XDT, int PDT, bool GATED>
+template <int XDT, int PDT, bool GATED, int BDT = XDT>
 __device__ __forceinline__ void load_input8(const PrepParams& p, int64_t row, int64_t goff, int64_t j,
                                             float (&v)[8]) {
   const int64_t e = row * p.k + j;
   load8<XDT>(p.x, e, v);
   if constexpr (GATED) {
     float b[8], g[8];
-    load8<XDT>(p.branch, e, b);
+    load8<BDT>(p.branch, e, b);
     load8<PDT>(p.gate, goff + j, g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = v[i] + b[i] * g[i];
@@ -188,8 +188,9 @@ __device__ __forceinline__ void decode8(const Raw8<DT>& r, float (&v)[8]) {
 
 // Fused kernel: NCH chunks of EPC elements per lane under layout L.  Every global load of
 // the row (X, branch, gate, gamma, scale, shift, signs) is issued up front, so a row waits
-// for memory once.
-template <class L, int XDT, int PDT, int B, int NCH, bool GATED>
+// for memory once.  BDT is the branch dtype: XDT, or FP32 for a branch of another float dtype
+// (the host widens BF16/FP16 branches exactly), so float(branch) is the same value either way.
+template <class L, int XDT, int PDT, int B, int NCH, bool GATED, int BDT = XDT>
 __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int64_t rows) {
   __shared__ float red[3 * kWaves];  // one slot per block reduction
   constexpr int EPC = Shape<B>::EPC;
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
   const int64_t toff = p.row_map ? static_cast<int64_t>(p.row_map[row]) * p.k : 0;
   bool live[N8];
   Raw8<XDT> xr[N8];
-  Raw8<XDT> br[GATED ? N8 : 1];
+  Raw8<BDT> br[GATED ? N8 : 1];
   Raw8<PDT> gr[GATED ? N8 : 1], gam[N8], scl[N8], shf[N8];
   uint2 sgn[N8];
 #pragma unroll
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
     if (live[g]) {
       xr[g] = fetch8<XDT>(p.x, row * p.k + j);
       if constexpr (GATED) {
-        br[g] = fetch8<XDT>(p.branch, row * p.k + j);
+        br[g] = fetch8<BDT>(p.branch, row * p.k + j);
         gr[g] = fetch8<PDT>(p.gate, goff + j);
       }
       gam[g] = fetch8<PDT>(p.gamma, j);
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
       decode8<XDT>(xr[g], t);
       if constexpr (GATED) {
         float b[8], gt[8];
-        decode8<XDT>(br[g], b);
+        decode8<BDT>(br[g], b);
         decode8<PDT>(gr[g], gt);
 #pragma unroll
         for (int i = 0; i < 8; ++i) t[i] = t[i] + b[i] * gt[i];
@@ -364,8 +365,8 @@ __global__ __launch_bounds__(kThreads) void norm_modulate_kernel(PrepParams p, i
   }
 }
 
-// Staged gated residual add (gated_residual.metal): 8 elements per thread.
-template <int XDT, int PDT>
+// Staged gated residual add (gated_residual.metal): 8 elements per thread, branch dtype BDT.
+template <int XDT, int PDT, int BDT>
 __global__ __launch_bounds__(kThreads) void gated_residual_kernel(PrepParams p, int64_t total_chunks) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (c >= total_chunks) return;
@@ -373,20 +374,20 @@ __global__ __launch_bounds__(kThreads) void gated_residual_kernel(PrepParams p, 
   const int64_t row = e / p.k, j = e - row * p.k;
   const int64_t goff = p.gate_map ? static_cast<int64_t>(p.gate_map[row]) * p.k : 0;
   float v[8];
-  load_input8<XDT, PDT, true>(p, row, goff, j, v);  // writes R_next
+  load_input8<XDT, PDT, true, BDT>(p, row, goff, j, v);  // writes R_next
 }
 
-template <int XDT, int PDT, int B, bool GATED>
+template <int XDT, int PDT, int B, bool GATED, int BDT>
 int launch_fused(const PrepParams& p, int64_t rows, hipStream_t st) {
   constexpr int EPC = Shape<B>::EPC;
   const dim3 block(kThreads);
   const int64_t per_thread = (p.k / EPC + kThreads - 1) / kThreads;
   const dim3 grid(static_cast<unsigned>(rows));
-  if (per_thread <= 1) fused_prep_kernel<GroupRow, XDT, PDT, B, 1, GATED><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 2) fused_prep_kernel<GroupRow, XDT, PDT, B, 2, GATED><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 3) fused_prep_kernel<GroupRow, XDT, PDT, B, 3, GATED><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 4) fused_prep_kernel<GroupRow, XDT, PDT, B, 4, GATED><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 8) fused_prep_kernel<GroupRow, XDT, PDT, B, 8, GATED><<<grid, block, 0, st>>>(p, rows);
+  if (per_thread <= 1) fused_prep_kernel<GroupRow, XDT, PDT, B, 1, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 2) fused_prep_kernel<GroupRow, XDT, PDT, B, 2, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 3) fused_prep_kernel<GroupRow, XDT, PDT, B, 3, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 4) fused_prep_kernel<GroupRow, XDT, PDT, B, 4, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
+  else if (per_thread <= 8) fused_prep_kernel<GroupRow, XDT, PDT, B, 8, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
   else {
     set_error("m5k_norm_hadamard_quantize: K=%lld exceeds the register-resident row limit %d", (long long)p.k,
               8 * kThreads * EPC);
@@ -395,29 +396,33 @@ int launch_fused(const PrepParams& p, int64_t rows, hipStream_t st) {
   return launch_status("m5k_norm_hadamard_quantize");
 }
 
-template <int XDT, int PDT, bool GATED>
+template <int XDT, int PDT, bool GATED, int BDT = XDT>
 int fused_by_block(int block, const PrepParams& p, int64_t rows, hipStream_t st) {
   switch (block) {
-    case 32: return launch_fused<XDT, PDT, 32, GATED>(p, rows, st);
-    case 64: return launch_fused<XDT, PDT, 64, GATED>(p, rows, st);
-    case 128: return launch_fused<XDT, PDT, 128, GATED>(p, rows, st);
-    case 256: return launch_fused<XDT, PDT, 256, GATED>(p, rows, st);
-    case 512: return launch_fused<XDT, PDT, 512, GATED>(p, rows, st);
-    case 1024: return launch_fused<XDT, PDT, 1024, GATED>(p, rows, st);
+    case 32: return launch_fused<XDT, PDT, 32, GATED, BDT>(p, rows, st);
+    case 64: return launch_fused<XDT, PDT, 64, GATED, BDT>(p, rows, st);
+    case 128: return launch_fused<XDT, PDT, 128, GATED, BDT>(p, rows, st);
+    case 256: return launch_fused<XDT, PDT, 256, GATED, BDT>(p, rows, st);
+    case 512: return launch_fused<XDT, PDT, 512, GATED, BDT>(p, rows, st);
+    case 1024: return launch_fused<XDT, PDT, 1024, GATED, BDT>(p, rows, st);
     default: set_error("m5k_norm_hadamard_quantize: unsupported block %d", block); return M5K_EINVAL;
   }
 }
 
+// branch_dtype is XDT or M5K_F32 (checked by the entry point).
 template <int XDT, int PDT>
-int fused_dispatch(int block, const PrepParams& p, int64_t rows, hipStream_t st) {
-  return p.branch ? fused_by_block<XDT, PDT, true>(block, p, rows, st)
-                  : fused_by_block<XDT, PDT, false>(block, p, rows, st);
+int fused_dispatch(int block, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
+  if (!p.branch) return fused_by_block<XDT, PDT, false>(block, p, rows, st);
+  if constexpr (XDT != M5K_F32) {
+    if (branch_dtype == M5K_F32) return fused_by_block<XDT, PDT, true, M5K_F32>(block, p, rows, st);
+  }
+  return fused_by_block<XDT, PDT, true>(block, p, rows, st);
 }
 
 template <int XDT>
-int fused_by_param(int pdt, int block, const PrepParams& p, int64_t rows, hipStream_t st) {
-  return pdt == M5K_BF16 ? fused_dispatch<XDT, M5K_BF16>(block, p, rows, st)
-                         : fused_dispatch<XDT, M5K_F32>(block, p, rows, st);
+int fused_by_param(int pdt, int block, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
+  return pdt == M5K_BF16 ? fused_dispatch<XDT, M5K_BF16>(block, branch_dtype, p, rows, st)
+                         : fused_dispatch<XDT, M5K_F32>(block, branch_dtype, p, rows, st);
 }
 
 template <int XDT, int PDT>
@@ -442,18 +447,27 @@ int norm_by_param(int pdt, const PrepParams& p, int64_t rows, hipStream_t st) {
   return pdt == M5K_BF16 ? launch_norm<XDT, M5K_BF16>(p, rows, st) : launch_norm<XDT, M5K_F32>(p, rows, st);
 }
 
-template <int XDT, int PDT>
+template <int XDT, int PDT, int BDT>
 int launch_gate(const PrepParams& p, int64_t rows, hipStream_t st) {
   const int64_t chunks = rows * p.k / 8;
   const int64_t blocks = (chunks + kThreads - 1) / kThreads;
   M5K_REQUIRE(blocks <= 0x7FFFFFFF, "m5k_gated_residual_add: input too large");
-  gated_residual_kernel<XDT, PDT><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st>>>(p, chunks);
+  gated_residual_kernel<XDT, PDT, BDT><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st>>>(p, chunks);
   return launch_status("m5k_gated_residual_add");
 }
 
-template <int XDT>
+template <int XDT, int BDT>
 int gate_by_param(int pdt, const PrepParams& p, int64_t rows, hipStream_t st) {
-  return pdt == M5K_BF16 ? launch_gate<XDT, M5K_BF16>(p, rows, st) : launch_gate<XDT, M5K_F32>(p, rows, st);
+  return pdt == M5K_BF16 ? launch_gate<XDT, M5K_BF16, BDT>(p, rows, st) : launch_gate<XDT, M5K_F32, BDT>(p, rows, st);
+}
+
+// branch_dtype is XDT or M5K_F32 (checked by the entry point).
+template <int XDT>
+int gate_by_branch(int pdt, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
+  if constexpr (XDT != M5K_F32) {
+    if (branch_dtype == M5K_F32) return gate_by_param<XDT, M5K_F32>(pdt, p, rows, st);
+  }
+  return gate_by_param<XDT, XDT>(pdt, p, rows, st);
 }
 
 bool a16(const void* ptr) { return ptr == nullptr || aligned16(ptr); }
@@ -477,7 +491,8 @@ using namespace m5k;
 using namespace m5k::prep;
 
 extern "C" int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t rows, int64_t k, const void* branch,
-                                          const void* gate, const int32_t* gate_row_map, const void* gamma,
+                                          int branch_dtype, const void* gate, const int32_t* gate_row_map,
+                                          const void* gamma,
                                           const void* scale, const void* shift, int param_dtype,
                                           const int32_t* row_map, const int8_t* signs, int block, int norm,
                                           float epsilon, int round_to_input, int8_t* q, float* scales,
@@ -489,6 +504,8 @@ extern "C" int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t ro
   M5K_REQUIRE(block >= 32 && block <= 1024 && (block & (block - 1)) == 0 && k % block == 0,
               "%s: block %d must be a power of two in [32,1024] dividing K", name, block);
   M5K_REQUIRE(!branch || (gate && residual_out), "%s: gated prep needs gate and residual_out", name);
+  M5K_REQUIRE(!branch || branch_dtype == x_dtype || branch_dtype == M5K_F32,
+              "%s: branch dtype %d must be the input dtype or F32", name, branch_dtype);
   M5K_REQUIRE(epsilon > 0.0f, "%s: epsilon must be positive", name);
   M5K_REQUIRE(a16(x) && a16(branch) && a16(gate) && a16(gamma) && a16(scale) && a16(shift) && a16(residual_out) &&
                   (reinterpret_cast<uintptr_t>(signs) & 7u) == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0,
@@ -497,9 +514,9 @@ extern "C" int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t ro
                nullptr, k, epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0};
   hipStream_t st = as_stream(stream);
   switch (x_dtype) {
-    case M5K_BF16: return fused_by_param<M5K_BF16>(param_dtype, block, p, rows, st);
-    case M5K_F16: return fused_by_param<M5K_F16>(param_dtype, block, p, rows, st);
-    default: return fused_by_param<M5K_F32>(param_dtype, block, p, rows, st);
+    case M5K_BF16: return fused_by_param<M5K_BF16>(param_dtype, block, branch_dtype, p, rows, st);
+    case M5K_F16: return fused_by_param<M5K_F16>(param_dtype, block, branch_dtype, p, rows, st);
+    default: return fused_by_param<M5K_F32>(param_dtype, block, branch_dtype, p, rows, st);
   }
 }
 
@@ -523,19 +540,21 @@ extern "C" int m5k_norm_modulate(const void* x, int x_dtype, int64_t rows, int64
 }
 
 extern "C" int m5k_gated_residual_add(const void* residual, int dtype, int64_t rows, int64_t k, const void* branch,
-                                      const void* gate, int gate_dtype, const int32_t* gate_row_map, void* out,
-                                      void* stream) {
+                                      int branch_dtype, const void* gate, int gate_dtype,
+                                      const int32_t* gate_row_map, void* out, void* stream) {
   clear_error();
   const char* name = "m5k_gated_residual_add";
   if (int rc = check_common(residual, dtype, rows, k, gate_dtype, name)) return rc;
   M5K_REQUIRE(branch && gate && out, "%s: null pointer", name);
+  M5K_REQUIRE(branch_dtype == dtype || branch_dtype == M5K_F32, "%s: branch dtype %d must be the residual dtype or F32",
+              name, branch_dtype);
   M5K_REQUIRE(a16(residual) && a16(branch) && a16(gate) && a16(out), "%s: misaligned buffers", name);
   PrepParams p{residual, branch, gate, gate_row_map, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                out,      nullptr, k,   1.0f,         0,       0};
   hipStream_t st = as_stream(stream);
   switch (dtype) {
-    case M5K_BF16: return gate_by_param<M5K_BF16>(gate_dtype, p, rows, st);
-    case M5K_F16: return gate_by_param<M5K_F16>(gate_dtype, p, rows, st);
-    default: return gate_by_param<M5K_F32>(gate_dtype, p, rows, st);
+    case M5K_BF16: return gate_by_branch<M5K_BF16>(gate_dtype, branch_dtype, p, rows, st);
+    case M5K_F16: return gate_by_branch<M5K_F16>(gate_dtype, branch_dtype, p, rows, st);
+    default: return gate_by_branch<M5K_F32>(gate_dtype, branch_dtype, p, rows, st);
   }
 }

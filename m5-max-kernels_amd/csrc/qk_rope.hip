@@ -325,8 +325,7 @@ int launch_fused(const void* a, const void* b, int64_t m, int64_t n, int64_t k, 
                  const QkParams& p, hipStream_t st) {
   const int64_t kb = k * Traits<MODE>::elem_bytes;
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  const bool aligned = kb % 16 == 0 && aligned16(a) && aligned16(b) && m * kb < (int64_t(1) << 31) &&
-                       n * kb < (int64_t(1) << 31);
+  const bool aligned = gemm::detail::dma_ok(a, b, kb);
   const dim3 grid(static_cast<unsigned>(tiles)), block(KernelGrid::THREADS);
   auto* A = static_cast<const uint8_t*>(a);
   auto* B = static_cast<const uint8_t*>(b);

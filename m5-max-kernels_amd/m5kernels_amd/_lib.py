@@ -49,10 +49,10 @@ SIGNATURES = {
     "m5k_hadamard_rotate": [_p, _i32, _i64, _i64, _i32, _p, _p, _p],
     "m5k_hadamard_quantize_rows": [_p, _i32, _i64, _i64, _i32, _p, _p, _p, _p],
     "m5k_norm_hadamard_quantize": [
-        _p, _i32, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _p,
+        _p, _i32, _i64, _i64, _p, _i32, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _p,
     ],
     "m5k_norm_modulate": [_p, _i32, _i64, _i64, _p, _p, _p, _i32, _p, _i32, _f32, _i32, _p, _p],
-    "m5k_gated_residual_add": [_p, _i32, _i64, _i64, _p, _p, _i32, _p, _p, _p],
+    "m5k_gated_residual_add": [_p, _i32, _i64, _i64, _p, _i32, _p, _i32, _p, _p, _p],
     "m5k_projection_qk_rope": [_p, _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i32, _f32, _p, _p],
     "m5k_qk_norm_rope": [_p, _i64, _i64, _p, _p, _p, _i32, _f32, _p, _p],
 }

@@ -3,8 +3,8 @@
 Drop-in mirror of the reference's ``hadamard.rotate`` (src/m5kernels/hadamard.py:33-77):
 Y = (X * signs) blockdiag(H_B) in FP32 for X[rows, K] (bf16/fp16/fp32), shared int8 +-1
 signs[K], B in {32, ..., 1024}, K % B == 0, no padding.  ``implementation`` keeps the
-reference's switch: "hip" (alias "metal") selects the gfx950 kernel; "mlx" named Apple's
-built-in transform and raises NotImplementedError here.
+reference's switch and default: "metal" (the default; alias "hip") selects the gfx950 kernel;
+"mlx" named Apple's built-in transform and raises NotImplementedError here.
 
 ``rotate_quantize`` is the fused rotation + per-row INT8 quantizer: it returns exactly
 ``quantize(rotate(x, B, signs), "int8")`` without materializing the FP32 rotation.
@@ -41,7 +41,7 @@ def _validate(x, block_size, signs):
     return block_size
 
 
-def rotate(x, block_size, signs, implementation="hip"):
+def rotate(x, block_size, signs, implementation="metal"):
     """Return FP32 X D H for nonempty X[rows, K] (hadamard.py:33-77)."""
     block_size = _validate(x, block_size, signs)
     if implementation == "mlx":

@@ -34,7 +34,7 @@ def _workload(args):
     import torch
 
     from . import experiments
-    from .cli import _with_hadamard
+    from .cli import hadamard_overrides
     from .engine import IMPLEMENTATION_LIMIT, all_finite
     from .numerics import metrics
     from .workloads import load
@@ -42,7 +42,7 @@ def _workload(args):
     cases = [c for c in load(args.suite)["cases"] if c["id"] == args.case]
     if len(cases) != 1:
         raise ValueError("select one exact case id")
-    case = _with_hadamard(cases[0], args) if args.backend == "mpp-hadamard" else cases[0]
+    case = hadamard_overrides(cases[0], args) if args.backend == "mpp-hadamard" else cases[0]
     prepare = experiments.PREPARE.get(case["op"], experiments.prepare_unsupported)
     fn, check, expected, original, stages, meta = prepare(case, args.backend, args.precision, args.seed, "normal",
                                                           tuple(args.tile))

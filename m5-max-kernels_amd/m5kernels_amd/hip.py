@@ -18,7 +18,11 @@ Differences that follow from the platform, not the contract:
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import functools
+import os
+import threading
 
 import torch
 
@@ -152,6 +156,35 @@ def tail_split_plan(m, n, k, cus=256):
 _PLAN_DTYPES = {"int8": _lib.I8, "fp8": _lib.U8, "bf16": _lib.BF16, "fp16": _lib.F16, "fp32": _lib.F32}
 SCHEDULES = ("plain", "mixed", "narrow")
 
+_override = threading.local()
+
+
+@contextlib.contextmanager
+def launch_override(schedule=None, splits=None):
+    """Fix the gfx950 GEMM launch for the calls made inside the block: `schedule` ("plain",
+    "mixed" or "narrow", read by the library from M5K_GEMM_SCHEDULE on every call) and, for
+    the W8A8 linear, the split-K count `splits` (1: no split; the INT32 partials are exact, so
+    every choice gives the same bits).  None keeps the library's own plan.  These are the knobs
+    the harness tuner searches; the environment variable is process-wide, so the block is meant
+    for one thread at a time."""
+    if schedule is not None and schedule not in SCHEDULES:
+        raise ValueError(f"unknown GEMM schedule {schedule!r}")
+    if splits is not None and (isinstance(splits, bool) or not isinstance(splits, int) or not 1 <= splits <= 64):
+        raise ValueError("splits must be an integer in [1, 64]")
+    saved_env = os.environ.get("M5K_GEMM_SCHEDULE")
+    saved_splits = getattr(_override, "splits", None)
+    if schedule is not None:
+        os.environ["M5K_GEMM_SCHEDULE"] = schedule
+    _override.splits = splits
+    try:
+        yield
+    finally:
+        _override.splits = saved_splits
+        if saved_env is None:
+            os.environ.pop("M5K_GEMM_SCHEDULE", None)
+        else:
+            os.environ["M5K_GEMM_SCHEDULE"] = saved_env
+
 
 def launch_plan(mode, m, n, cus=256):
     """The library's GEMM schedule for an [m, n] output on `cus` CUs (m5k_gemm_launch_plan;
@@ -161,8 +194,28 @@ def launch_plan(mode, m, n, cus=256):
     return SCHEDULES[sched.value], full.value
 
 
+@functools.lru_cache(maxsize=None)
+def _cu_count_of(index):
+    return torch.cuda.get_device_properties(index).multi_processor_count
+
+
 def _cu_count(device):
-    return torch.cuda.get_device_properties(device).multi_processor_count
+    return _cu_count_of(device.index if device.index is not None else torch.cuda.current_device())
+
+
+@functools.lru_cache(maxsize=4096)
+def _i8_schedule(m, n, k, cus, env):
+    """Host schedule of an aligned W8A8 linear, cached per shape, CU count and the library's
+    schedule switches `env` (M5K_GEMM_MIXED_TILES, M5K_GEMM_NARROW_TILES, M5K_GEMM_SCHEDULE):
+    (splits, tail), with
+    tail = (rows of the plain launch, splits of the rest) or None."""
+    splits = splitk_plan(m, n, k, cus)
+    # The library's mixed and narrow launches refill a partial last round without INT32
+    # partials and measured faster wherever both apply; the split-K tail takes the rest.
+    tail = None
+    if splits == 1 and launch_plan("int8", m, n, cus)[0] == "plain":
+        tail = tail_split_plan(m, n, k, cus)
+    return splits, tail
 
 
 def gemm(
@@ -279,12 +332,16 @@ def gemm(
         if bias is not None:
             bias = _lib.device_tensor(bias, "bias")
             bias_row_map = None if bias_row_map is None else _lib.device_tensor(bias_row_map, "bias_row_map")
+        # Split-K and the tail split run the direct-to-LDS main loop only (m5k_gemm_i8_splitk
+        # rejects other operands): 16-byte aligned rows and bases.
         aligned = k % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
-        splits = splitk_plan(m, n, k, _cu_count(a.device)) if aligned else 1
-        # The library's mixed and narrow launches refill a partial last round without INT32
-        # partials and measured faster wherever both apply; the split-K tail takes the rest.
-        cus = _cu_count(a.device) if aligned and splits == 1 else 0
-        tail = tail_split_plan(m, n, k, cus) if cus and launch_plan("int8", m, n, cus)[0] == "plain" else None
+        splits, tail = 1, None
+        forced_splits = getattr(_override, "splits", None)
+        if aligned and forced_splits is not None:
+            splits = forced_splits
+        elif aligned:
+            env = tuple(os.environ.get(v) for v in ("M5K_GEMM_MIXED_TILES", "M5K_GEMM_NARROW_TILES", "M5K_GEMM_SCHEDULE"))
+            splits, tail = _i8_schedule(m, n, k, _cu_count(a.device), env)
         if tail is not None:
             # Whole tile rows in full rounds, then the remaining rows split along K.  Every
             # row-indexed operand is sliced at the same row; both launches are bit-exact.

@@ -14,8 +14,9 @@ Platform notes (contract unchanged):
   the reference; the gfx950 kernel always keeps the row in registers with 256 lanes.
 * gamma/scale/shift/gate are consumed as FP32 (bf16 tables are read natively; fp16 tables
   are widened to FP32 first, exactly).
-* ``branch`` must have the residual's dtype (the reference also accepts a different float
-  dtype; that case raises NotImplementedError here).
+* A ``branch`` of another float dtype than the residual is widened to FP32 (exact for
+  BF16/FP16) and read as FP32 by the kernel: ``float(branch)`` is the same value, so the
+  FP32 product-then-add and the single residual-dtype cast are unchanged.
 * K must be a multiple of 8 (always true with a Hadamard block; checked for unfused_norm
   and gated_residual_add).
 """
@@ -102,8 +103,6 @@ def _validate_gate(residual, branch, gate, gate_row_map):
             raise ValueError("mapped gate must have nonempty shape [P,K]")
         if tuple(gate_row_map.shape) != (residual.shape[0],) or gate_row_map.dtype != torch.int32:
             raise ValueError("gate_row_map must be an int32 vector of length M")
-    if branch.dtype != residual.dtype:
-        raise NotImplementedError("branch must have the residual's dtype on MI355X")
 
 
 def _params(*tensors):
@@ -122,6 +121,14 @@ def _map(t, name):
     return None if t is None else _lib.device_tensor(t, name)
 
 
+def _branch(branch, residual):
+    """Device branch and its dtype code: the residual's dtype, else exactly widened to FP32."""
+    if branch.dtype != residual.dtype:
+        branch = branch.to(torch.float32)
+    branch = _lib.aligned_device_tensor(branch, "branch")
+    return branch, _lib.dtype_code(branch)
+
+
 def _norm_code(norm):
     return _lib.NORM_LAYER if norm == "layer" else _lib.NORM_RMS
 
@@ -134,14 +141,14 @@ def _prep(x, gamma, scale, shift, signs, block_size, norm, epsilon, round_output
     rows, k = x.shape
     q = torch.empty((rows, k), dtype=torch.int8, device=x.device)
     s = torch.empty((rows,), dtype=torch.float32, device=x.device)
-    r_next = None
+    r_next, branch_code = None, _lib.dtype_code(x)
     if branch is not None:
-        branch = _lib.aligned_device_tensor(branch, "branch")
+        branch, branch_code = _branch(branch, x)
         r_next = torch.empty_like(x)
     _lib.call(
         "m5k_norm_hadamard_quantize",
         _lib.ptr(x), _lib.dtype_code(x), rows, k,
-        _lib.ptr(branch), _lib.ptr(gate_d), _lib.ptr(_map(gate_row_map, "gate_row_map")),
+        _lib.ptr(branch), branch_code, _lib.ptr(gate_d), _lib.ptr(_map(gate_row_map, "gate_row_map")),
         _lib.ptr(gamma_d), _lib.ptr(scale_d), _lib.ptr(shift_d), pdt, _lib.ptr(_map(row_map, "row_map")),
         _lib.ptr(signs), int(block_size), _norm_code(norm), float(epsilon), 1 if round_output == "input" else 0,
         _lib.ptr(q), _lib.ptr(s), _lib.ptr(r_next), _lib.stream_of(x),
@@ -216,13 +223,13 @@ def gated_residual_add(residual, branch, gate, *, gate_row_map=None, threads=256
     if residual.shape[1] % 8:
         raise NotImplementedError("K must be a multiple of 8 on MI355X")
     residual = _lib.aligned_device_tensor(residual, "residual")
-    branch = _lib.aligned_device_tensor(branch, "branch")
+    branch, branch_code = _branch(branch, residual)
     pdt, (gate_d,) = _params(gate)
     out = torch.empty_like(residual)
     rows, k = residual.shape
     _lib.call(
         "m5k_gated_residual_add",
-        _lib.ptr(residual), _lib.dtype_code(residual), rows, k, _lib.ptr(branch), _lib.ptr(gate_d), pdt,
+        _lib.ptr(residual), _lib.dtype_code(residual), rows, k, _lib.ptr(branch), branch_code, _lib.ptr(gate_d), pdt,
         _lib.ptr(_map(gate_row_map, "gate_row_map")), _lib.ptr(out), _lib.stream_of(residual),
     )
     return out

@@ -448,6 +448,11 @@ def c_lib() -> ctypes.CDLL:
             "oracle_i8_epilogue": [p, p, p, i64, i64, p, p, p, p, p, i32, p],
             "oracle_w8a8_linear_bf16": [p, p, p, i64, i64, i64, p, p, p],
             "oracle_hadamard_f32": [p, i64, i64, i32, p, p],
+            "oracle_f16_round_array": [p, i64, p],
+            "oracle_prep_rows": [p, i32, p, p, p, p, p, p, p, p, i64, i64, i32, i32, i32, ctypes.c_float, i32, p, p,
+                                 p, p],
+            "oracle_qk_norm_rope": [p, i64, i64, p, p, p, i32, ctypes.c_float, p],
+            "oracle_qkv_norm_rope": [p, i64, i64, p, p, p, p, i32, ctypes.c_float, p, p, p],
         }.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -570,3 +575,109 @@ def rms_quantize_reference(x, gamma, signs=None, block_size=1, eps=1e-5):
         "inverse_rms": inverse_rms,
         "unscaled_scales": unscaled_scales,
     }
+
+
+# ----------------------------------------------------------------------------------------
+# Fixed-order FP32 prep and Q/K epilogue (liboracle.so; the order is stated in m5k_oracle.c)
+# ----------------------------------------------------------------------------------------
+
+_DT_CODES = {"fp32": 0, "fp16": 1, "bf16": 2}
+
+
+def c_f16_round(x):
+    """FP32 values rounded to binary16 (nearest even) and back, by the C oracle."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    c_lib().oracle_f16_round_array(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def c_prep_rows(x, gamma, scale, shift, signs, block, *, dtype="bf16", norm="rms", eps=1e-5, round_output="input",
+                row_map=None, branch=None, gate=None, gate_row_map=None, with_modulated=False):
+    """Fused (gated) AdaLN / RMS prep in the fixed FP32 order of the library (norm_hadamard.py:
+    122-265): returns (codes, scales) or (codes, scales, r_next FP32 values) when `branch` is given,
+    plus the FP32 modulation before the O cast last when `with_modulated`.
+    x, branch, gate, gamma, scale, shift are FP32 values (exact decodes of their storage dtypes);
+    `dtype` names x's storage dtype (the R and O casts)."""
+    f32 = lambda t: None if t is None else np.ascontiguousarray(t, dtype=np.float32)  # noqa: E731
+    i32 = lambda t: None if t is None else np.ascontiguousarray(t, dtype=np.int32)  # noqa: E731
+    x, branch, gate, gamma, scale, shift = map(f32, (x, branch, gate, gamma, scale, shift))
+    signs = np.ascontiguousarray(signs, dtype=np.int8)
+    rows, k = x.shape
+    q = np.empty((rows, k), dtype=np.int8)
+    s = np.empty(rows, dtype=np.float32)
+    r_next = np.empty((rows, k), dtype=np.float32) if branch is not None else None
+    modulated = np.empty((rows, k), dtype=np.float32) if with_modulated else None
+    c_lib().oracle_prep_rows(
+        _ptr(x), _DT_CODES[dtype], _ptr(branch), _ptr(gate), _ptr(i32(gate_row_map)), _ptr(gamma), _ptr(scale),
+        _ptr(shift), _ptr(i32(row_map)), _ptr(signs), rows, k, int(block), max(8, int(block) // 64),
+        1 if norm in ("layer", "layernorm") else 0, float(eps), 1 if round_output == "input" else 0, _ptr(q), _ptr(s),
+        _ptr(r_next), _ptr(modulated))
+    out = (q, s) if branch is None else (q, s, r_next)
+    return out + (modulated,) if with_modulated else out
+
+
+def c_qk_norm_rope(z_bits, gamma_bits, cos_bits, sin_bits, *, epsilon=1e-6):
+    """Q/K epilogue in the library's FP32 order on a BF16 projection z [M, N] (uint16 bits):
+    head-major [N/128, M, 128] BF16 bits (qk_rope_reference.py:45-134 order-fixed)."""
+    z = np.ascontiguousarray(z_bits, dtype=np.uint16)
+    m, n = z.shape
+    cos_bits = np.ascontiguousarray(cos_bits, dtype=np.uint16)
+    sin_bits = np.ascontiguousarray(sin_bits, dtype=np.uint16)
+    rope_half = cos_bits.shape[1] if cos_bits.ndim == 2 else 0
+    y = np.empty((n // 128, m, 128), dtype=np.uint16)
+    c_lib().oracle_qk_norm_rope(_ptr(z), m, n, _ptr(np.ascontiguousarray(gamma_bits, dtype=np.uint16)),
+                                _ptr(cos_bits), _ptr(sin_bits), rope_half, float(epsilon), _ptr(y))
+    return y
+
+
+def c_qkv_norm_rope(z_bits, q_gamma_bits, k_gamma_bits, cos_bits, sin_bits, *, epsilon=1e-6):
+    """Grouped Q/K/V epilogue (weight rows [head, stream, 128]) on z [M, heads * 384] BF16 bits:
+    (q, k, v) head-major [heads, M, 128] BF16 bits."""
+    z = np.ascontiguousarray(z_bits, dtype=np.uint16)
+    m, n = z.shape
+    heads = n // 384
+    cos_bits = np.ascontiguousarray(cos_bits, dtype=np.uint16)
+    sin_bits = np.ascontiguousarray(sin_bits, dtype=np.uint16)
+    outs = [np.empty((heads, m, 128), dtype=np.uint16) for _ in range(3)]
+    c_lib().oracle_qkv_norm_rope(_ptr(z), m, heads, _ptr(np.ascontiguousarray(q_gamma_bits, dtype=np.uint16)),
+                                 _ptr(np.ascontiguousarray(k_gamma_bits, dtype=np.uint16)), _ptr(cos_bits),
+                                 _ptr(sin_bits), cos_bits.shape[1], float(epsilon), *map(_ptr, outs))
+    return tuple(outs)
+
+
+# ----------------------------------------------------------------------------------------
+# oracle/_ref: the reference's own float64 grouped Q/K/V header (integrations/h3/
+# qkv_reference.h), compiled where it lies by `make -C oracle ref`
+# ----------------------------------------------------------------------------------------
+
+REF_QKV_PATH = HERE / "_ref" / "libqkv_ref.so"
+_REF_QKV = None
+
+
+def ref_qkv_lib():
+    """The compiled reference header, or None when oracle/_ref was not built."""
+    global _REF_QKV
+    if _REF_QKV is None and REF_QKV_PATH.exists():
+        lib = ctypes.CDLL(str(REF_QKV_PATH))
+        p, i64 = ctypes.c_void_p, ctypes.c_int64
+        lib.ref_qkv_postprocess.argtypes = [p, i64, ctypes.c_uint, p, p, p, ctypes.c_double, p]
+        lib.ref_qkv_postprocess.restype = None
+        lib.ref_qkv_h256.argtypes = [p, ctypes.c_uint]
+        lib.ref_qkv_h256.restype = None
+        _REF_QKV = lib
+    return _REF_QKV
+
+
+def ref_qkv_postprocess(projection, stream, gamma_bits, cos_bits, sin_bits, epsilon):
+    """qvr_postprocess (qkv_reference.h:17-35) over rows of float64 head projections [rows, 128]
+    with rope half 48: BF16-rounded projection, float64 RMSNorm, gamma, RoPE, BF16 output
+    (returned as float64 values)."""
+    lib = ref_qkv_lib()
+    projection = np.ascontiguousarray(projection, dtype=np.float64)
+    rows = projection.shape[0]
+    out = np.empty_like(projection)
+    lib.ref_qkv_postprocess(_ptr(projection), rows, int(stream), _ptr(np.ascontiguousarray(gamma_bits, np.uint16)),
+                            _ptr(np.ascontiguousarray(cos_bits, np.uint16)),
+                            _ptr(np.ascontiguousarray(sin_bits, np.uint16)), float(epsilon), _ptr(out))
+    return out

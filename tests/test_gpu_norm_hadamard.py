@@ -251,3 +251,90 @@ def test_prep_configuration_shapes(device):
                     norm="layer", eps=1e-5, out_dtype=torch.bfloat16, row_map=rmap)
         staged = gated_residual_add(x, br, gate, gate_row_map=row_map)
         assert torch.equal(staged, upd)
+
+
+# ---- bit-exact against the fixed-order FP32 oracle (oracle_prep_rows) ---------------------------
+
+
+def _oracle_prep(x, gamma, scale, shift, signs, block, **kw):
+    f32 = lambda t: None if t is None else (t.float().cpu().numpy() if isinstance(t, torch.Tensor) else t)  # noqa: E731
+    dt = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[x.dtype]
+    for key in ("branch", "gate"):
+        if key in kw:
+            kw[key] = f32(kw[key])
+    for key in ("row_map", "gate_row_map"):
+        if kw.get(key) is not None:
+            kw[key] = np_of(kw[key])
+    return ref.c_prep_rows(f32(x), f32(gamma), f32(scale), f32(shift), np_of(signs), block, dtype=dt, **kw)
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("dtype", list(DT))
+@pytest.mark.parametrize("round_output", ["input", "fp32"])
+@pytest.mark.parametrize("block,width", [(32, 768), (128, 4096), (256, 5376), (512, 3072), (1024, 6144),
+                                         (64, 5120), (256, 16384)])
+def test_fused_prep_bit_exact_vs_fixed_order_oracle(norm, dtype, round_output, block, width, device):
+    """Codes and scales equal the oracle's fixed FP32 order bit for bit: lane chunks of
+    max(8, B/64) elements, the DPP row tree, fmaf squares and modulation, the O cast."""
+    rng = np.random.default_rng(block + width + len(dtype))
+    x = torch.from_numpy(rng.standard_normal((9, width), dtype=np.float32)).to(device).to(DT[dtype])
+    x[3, ::97] *= 60
+    gamma = (1 + 0.1 * torch.randn(width, device=device)).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(2, width, device=device)).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(2, width, device=device)).to(torch.bfloat16)
+    row_map = torch.tensor([0, 1] * 4 + [1], dtype=torch.int32, device=device)
+    signs = torch.from_numpy(ref.hadamard_signs(width, 5)).to(device)
+    q, s = fused_norm_hadamard_quantize(x, gamma, scale, shift, signs, block, norm=norm, round_output=round_output,
+                                        row_map=row_map)
+    oq, os_ = _oracle_prep(x, gamma, scale, shift, signs, block, norm=norm, round_output=round_output, row_map=row_map)
+    np.testing.assert_array_equal(np_of(q), oq)
+    np.testing.assert_array_equal(np_of(s), os_)
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("dtype,branch_dtype", [("bf16", "bf16"), ("bf16", "fp32"), ("bf16", "fp16"),
+                                                ("fp16", "bf16"), ("fp32", "bf16"), ("fp16", "fp16")])
+@pytest.mark.parametrize("mapped", [False, True])
+def test_gated_prep_mixed_branch_dtype_bit_exact(norm, dtype, branch_dtype, mapped, device):
+    """A branch of another float dtype than the residual: float(branch) enters the FP32 product
+    and add as is (norm_hadamard.py:184 accepts any float dtype); R_next, codes and scales equal
+    the fixed-order oracle, and the staged gated_residual_add equals R_next."""
+    rng = np.random.default_rng(401)
+    shape = (7, 5376)
+    rt = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(device).to(DT[dtype])
+    bt = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * 3).to(device).to(DT[branch_dtype])
+    gate = torch.from_numpy(rng.uniform(-0.7, 0.7, size=(3, 5376) if mapped else 5376).astype(np.float32))
+    gate = gate.to(device).to(torch.bfloat16)
+    gmap = torch.tensor([1, 0, 2, 2, 1, 0, 1], dtype=torch.int32, device=device) if mapped else None
+    gamma = (1 + 0.1 * torch.randn(5376, device=device)).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(5376, device=device)).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(5376, device=device)).to(torch.bfloat16)
+    signs = torch.from_numpy(ref.hadamard_signs(5376, 29)).to(device)
+    q, s, upd = fused_gated_residual_norm_hadamard_quantize(rt, bt, gate, gamma, scale, shift, signs, 256, norm=norm,
+                                                            gate_row_map=gmap)
+    assert upd.dtype == rt.dtype
+    oq, os_, orn = _oracle_prep(rt, gamma, scale, shift, signs, 256, norm=norm, branch=bt, gate=gate,
+                                gate_row_map=gmap)
+    np.testing.assert_array_equal(upd.float().cpu().numpy(), orn)
+    np.testing.assert_array_equal(np_of(q), oq)
+    np.testing.assert_array_equal(np_of(s), os_)
+    assert torch.equal(gated_residual_add(rt, bt, gate, gate_row_map=gmap), upd)
+
+
+def test_gated_residual_add_mixed_dtype_through_c_abi(device):
+    """m5k_gated_residual_add with an F32 branch beside a BF16 residual, called directly."""
+    from m5kernels_amd import _lib
+
+    rng = np.random.default_rng(5)
+    res = torch.from_numpy(rng.standard_normal((3, 256), dtype=np.float32)).to(device).to(torch.bfloat16)
+    branch = torch.from_numpy(rng.standard_normal((3, 256), dtype=np.float32)).to(device)
+    gate = torch.from_numpy(rng.uniform(-1, 1, 256).astype(np.float32)).to(device)
+    out = torch.empty_like(res)
+    _lib.call("m5k_gated_residual_add", _lib.ptr(res), _lib.BF16, 3, 256, _lib.ptr(branch), _lib.F32, _lib.ptr(gate),
+              _lib.F32, None, _lib.ptr(out), _lib.stream_of(res))
+    expected = ref.f32_to_bf16_bits((res.float().cpu().numpy() + branch.cpu().numpy() * gate.cpu().numpy())
+                                    .astype(np.float32))
+    np.testing.assert_array_equal(bits_of(out), expected)
+    with pytest.raises(RuntimeError, match="branch dtype"):
+        _lib.call("m5k_gated_residual_add", _lib.ptr(res), _lib.BF16, 3, 256, _lib.ptr(branch), _lib.F16,
+                  _lib.ptr(gate), _lib.F32, None, _lib.ptr(out), _lib.stream_of(res))

@@ -272,3 +272,61 @@ def test_short_m_routing_matches_fused_kernel(m, device):
               _lib.ptr(sb), _lib.ptr(gamma.contiguous()), _lib.ptr(cos.contiguous()), _lib.ptr(sin.contiguous()),
               cos.shape[1], float(np.float32(1e-6)), _lib.ptr(fused), _lib.stream_of(a))
     np.testing.assert_array_equal(bits_of(routed), bits_of(fused))
+
+
+# ---- bit-exact against the fixed-order FP32 oracle (oracle_qk_norm_rope / _qkv_) -------------
+
+
+@pytest.mark.parametrize("rope_half", [1, 5, 48, 64])
+@pytest.mark.parametrize("shape", [(17, 384, 96), (300, 640, 1024), (129, 256, 257)])
+def test_int8_fused_bit_exact_vs_fixed_order_oracle(rope_half, shape, device):
+    """INT8 fused projection: the oracle's exact INT32 projection through the FP32 dequant and
+    BF16 cast, then the epilogue's FP32 order (16-lane sum tree, IEEE 1/sqrt, split-half RoPE)."""
+    rng = np.random.default_rng(rope_half * 7 + shape[0])
+    m, n, k = shape
+    a, sa = quantize(torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device), "int8")
+    b, sb = quantize(torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32)).to(device), "int8")
+    gamma, cos, sin = _tables(rng, m, device, rope_half)
+    y = projection_qk_rope(a, b, gamma, cos, sin, "int8", a_scales=sa, b_scales=sb, epsilon=1e-6)
+    z = ref.c_i8_epilogue(ref.c_gemm_i8_acc(np_of(a), np_of(b)), np_of(sa), np_of(sb))
+    expected = ref.c_qk_norm_rope(z, bits_of(gamma), bits_of(cos), bits_of(sin), epsilon=float(np.float32(1e-6)))
+    np.testing.assert_array_equal(bits_of(y), expected)
+
+
+def test_staged_postprocess_bit_exact_vs_fixed_order_oracle(device):
+    """The staged epilogue on a given BF16 projection (zeros, outliers, R = 48)."""
+    rng = np.random.default_rng(9)
+    p_np = rng.standard_normal((40, 4 * 128), dtype=np.float32) * 2
+    p_np[0] = 0
+    p_np[1, ::31] *= 100
+    p = torch.from_numpy(p_np).to(device).to(torch.bfloat16)
+    gamma, cos, sin = _tables(rng, 40, device, 48)
+    y = qk_norm_rope(p, gamma, cos, sin, epsilon=1e-5)
+    expected = ref.c_qk_norm_rope(bits_of(p), bits_of(gamma), bits_of(cos), bits_of(sin),
+                                  epsilon=float(np.float32(1e-5)))
+    np.testing.assert_array_equal(bits_of(y), expected)
+
+
+@pytest.mark.parametrize("rope_half", [48, 5])
+@pytest.mark.parametrize("m,heads", [(300, 3), (4096, 32)])
+def test_grouped_qkv_bit_exact_vs_oracle(rope_half, m, heads, device):
+    """Grouped Q/K/V (weight rows [head, stream, 128]): Q and K equal the fixed-order oracle of
+    the INT8 projection bit for bit, V the BF16 projection (sampled rows at M 4096)."""
+    from m5kernels_amd import projection_qkv_rope
+
+    rng = np.random.default_rng(m + heads + rope_half)
+    k = 1024
+    x = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(device).to(torch.bfloat16)
+    w = torch.from_numpy((rng.standard_normal((heads * 384, k)) * 0.05).astype(np.float32)).to(device)
+    a, sa = quantize(x, "int8")
+    b, sb = quantize(w.to(torch.bfloat16), "int8")
+    q_gamma, cos, sin = _tables(rng, m, device, rope_half)
+    k_gamma = torch.from_numpy(rng.uniform(0.5, 1.5, 128).astype(np.float32)).to(device).to(torch.bfloat16)
+    q, kk, v = projection_qkv_rope(a, b, q_gamma, k_gamma, cos, sin, "int8", a_scales=sa, w_scales=sb)
+    rows = ref.sample_indices(m) if m > 512 else np.arange(m)
+    z = ref.c_i8_epilogue(ref.c_gemm_i8_acc(np_of(a[rows]), np_of(b)), np_of(sa[rows]), np_of(sb))
+    oq, ok, ov = ref.c_qkv_norm_rope(z, bits_of(q_gamma), bits_of(k_gamma), bits_of(cos[rows]), bits_of(sin[rows]),
+                                     epsilon=float(np.float32(1e-6)))
+    np.testing.assert_array_equal(bits_of(q[:, rows]), oq)
+    np.testing.assert_array_equal(bits_of(kk[:, rows]), ok)
+    np.testing.assert_array_equal(bits_of(v[:, rows]), ov)

@@ -209,6 +209,96 @@ def test_report_table(tmp_path, capsys):
     assert out[3] == "| b | mlx | bf16 | — | — | — | — | — | — | unsupported |"
 
 
+def test_tune_launch_space():
+    """The tuner's candidates are gfx950 launches: the library's plan, each forced schedule
+    (narrow only for the 16 x 16 MFMA modes) and, for INT8, split-K counts."""
+    case = {"id": "c", "op": "gemm", "m": 128, "n": 4096, "k": 16384}
+    int8 = cli.launch_space(case, "int8")
+    assert int8[0] == cli.Launch() and cli.Launch("narrow") in int8
+    splits = sorted(l.splits for l in int8 if l.splits)
+    assert splits and all(2 <= s <= 64 for s in splits)
+    fp8 = cli.launch_space(case, "fp8")
+    assert cli.Launch("narrow") not in fp8 and not any(l.splits for l in fp8)
+    assert len(set(int8)) == len(int8)
+    for launch in int8:
+        assert cli.Launch.from_record(launch.record()) == launch
+
+
+def test_launch_override_sets_and_restores(monkeypatch):
+    import os
+
+    from m5kernels_amd import hip
+
+    monkeypatch.delenv("M5K_GEMM_SCHEDULE", raising=False)
+    with hip.launch_override("narrow", 4):
+        assert os.environ["M5K_GEMM_SCHEDULE"] == "narrow" and hip._override.splits == 4
+        with hip.launch_override(None, None):
+            assert os.environ["M5K_GEMM_SCHEDULE"] == "narrow" and hip._override.splits is None
+        assert hip._override.splits == 4
+    assert "M5K_GEMM_SCHEDULE" not in os.environ and hip._override.splits is None
+    with pytest.raises(ValueError):
+        with hip.launch_override("diagonal"):
+            pass
+    with pytest.raises(ValueError):
+        with hip.launch_override(splits=0):
+            pass
+
+
+def _fake_run_case(times, calls):
+    """A stand-in for engine.run_case: records the call and the launch in force, and times
+    each launch by `times` (None: incorrect)."""
+    from m5kernels_amd import hip
+    import os
+
+    def run_case(c, backend, precision, seed=17, distribution="normal", warmup=3, repeat=10, tile=(64, 64, 4, 1)):
+        launch = cli.Launch(os.environ.get("M5K_GEMM_SCHEDULE"), getattr(hip._override, "splits", None))
+        calls.append((c["id"], backend, precision, seed, launch))
+        ms = times.get(launch, 1.0) if backend != "mlx" else 2.0
+        if ms is None:
+            return dict(case=c, backend=backend, precision=precision, status="incorrect", tile=list(tile))
+        return dict(case=c, backend=backend, precision=precision, status="ok", quality_pass=True, tile=list(tile),
+                    timing={"median_ms": ms}, stages={"online_activation_plus_gemm": {"median_ms": ms + 0.1}})
+    return run_case
+
+
+def test_tune_selects_fastest_launch_then_holdout_on_fresh_seed(tmp_path, monkeypatch):
+    times = {cli.Launch(): 1.0, cli.Launch("mixed"): 0.8, cli.Launch("plain"): None}
+    calls = []
+    monkeypatch.setattr(engine, "run_case", _fake_run_case(times, calls))
+    monkeypatch.setattr(engine, "environment", lambda: {})
+    out = tmp_path / "t.json"
+    rc = cli.main(["tune", "--suite", "h3", "--filter", "attn_q.m128", "--precisions", "int8", "--seed", "5",
+                   "--output", str(out)])
+    assert rc == 0
+    doc = json.loads(out.read_text())
+    sel = doc["selections"]
+    assert len(sel) == 1 and sel[0]["launch"] == {"schedule": "mixed", "splits": "auto"}
+    assert sel[0]["holdout"]["launch"] == sel[0]["launch"]
+    tuning = [c for c in calls if c[3] == 5]
+    holdout = [c for c in calls if c[3] == 6]
+    assert len(tuning) == len(cli.launch_space(doc["results"][0]["case"], "int8"))
+    assert holdout == [(sel[0]["case_id"], "mpp", "int8", 6, cli.Launch("mixed"))]
+    assert all("launch" in r for r in doc["results"])
+    # validate-selections re-runs the selected launch beside the BF16 framework baseline.
+    calls.clear()
+    out2 = tmp_path / "v.json"
+    assert cli.main(["validate-selections", str(out), "--seed", "29", "--output", str(out2)]) == 0
+    assert [c[1:] for c in calls] == [("mlx", "bf16", 29, cli.Launch()), ("mpp", "int8", 29, cli.Launch("mixed"))]
+    comparison = json.loads(out2.read_text())["comparisons"][0]
+    assert comparison["speedup"] == pytest.approx(2.0 / 0.9)
+
+
+def test_tune_fails_without_a_correct_launch(tmp_path, monkeypatch):
+    calls = []
+    monkeypatch.setattr(engine, "run_case", _fake_run_case({l: None for l in cli.launch_space(
+        {"m": 128, "n": 7168, "k": 5376}, "int8")}, calls))
+    monkeypatch.setattr(engine, "environment", lambda: {})
+    out = tmp_path / "t.json"
+    assert cli.main(["tune", "--suite", "h3", "--filter", "attn_q.m128", "--precisions", "int8",
+                     "--output", str(out)]) == 1
+    assert json.loads(out.read_text())["selections"] == []
+
+
 def test_write_result_never_replaces(tmp_path):
     p = tmp_path / "out.json"
     engine.write_result(p, {"a": 1})
