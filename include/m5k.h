@@ -120,7 +120,7 @@ int m5k_gemm_i8(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t 
  * contiguous ranges of K (1..64), the raw INT32 partial tiles go to workspace[splits][m][n]
  * (int32, caller-owned, at least splits*m*n elements), and a second kernel sums them in
  * split order and applies the identical epilogue.  INT32 sums are exact, so c is bit-identical
- * to m5k_gemm_i8's.  Needs k % 16 == 0, 16-byte aligned a/b, m*k and n*k < 2^31.  Same
+ * to m5k_gemm_i8's.  Needs k % 16 == 0 and 16-byte aligned a/b (any operand size).  Same
  * contract as metal.gemm(a, b, "int8", ...) (src/m5kernels/metal.py:158-269); the split is
  * this library's schedule for few-tile shapes (one or two 256-row tile rows).
  */
@@ -129,6 +129,22 @@ int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, i
                        const float* bias, const int32_t* bias_row_map, const void* residual,
                        const void* gate, const int32_t* gate_row_map, int splits, int32_t* workspace,
                        int64_t workspace_elems, void* stream);
+
+/*
+ * m5k_gemm_i8_splitk without the caller's workspace: the INT32 partials go to a scratch array
+ * of the library (M5K_SCRATCH_ELEMS int32 = 64 MiB per GPU, a static device array held until
+ * the process ends), so the call allocates nothing -- no hipMalloc, no hipFree, no allocating
+ * library routine.  No counterpart in the reference: it is for callers that cannot allocate
+ * (HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * splits * m * n must not exceed M5K_SCRATCH_ELEMS (M5K_EINVAL otherwise).  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race.  Results are bit-identical to m5k_gemm_i8_splitk and m5k_gemm_i8.
+ */
+#define M5K_SCRATCH_ELEMS (16 * 1024 * 1024)
+int m5k_gemm_i8_splitk_noalloc(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                               const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                               const float* bias, const int32_t* bias_row_map, const void* residual,
+                               const void* gate, const int32_t* gate_row_map, int splits, void* stream);
 
 /*
  * Launch plan of the MFMA GEMMs (host only, launches nothing).  No counterpart in the

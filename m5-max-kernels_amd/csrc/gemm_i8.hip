@@ -1,4 +1,7 @@
 // C-ABI entry points of the W8A8 (INT8 x INT8 -> INT32) linear; kernels in gemm_launch.h.
+#include <cstdio>
+#include <mutex>
+
 #include "gemm_launch.h"
 
 using namespace m5k;
@@ -57,6 +60,35 @@ extern "C" int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus,
   return M5K_OK;
 }
 
+namespace {
+
+// Split-K partials of m5k_gemm_i8_splitk_noalloc.  The name is a host-side stand-in: host code
+// uses only the per-device address that hipGetSymbolAddress returns.
+static __device__ __align__(256) int32_t scratch[M5K_SCRATCH_ELEMS];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int32_t* g_scratch[kMaxDevices] = {};
+
+// This GPU's copy of `scratch` (looked up once per device, with that device current).
+int scratch_of_current_device(int32_t** out, const char* name) {
+  int dev = -1;
+  M5K_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, "%s: no current HIP device (%d)",
+              name, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    M5K_REQUIRE(e == hipSuccess && ptr != nullptr, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name,
+                dev, hipGetErrorString(e));
+    g_scratch[dev] = static_cast<int32_t*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return M5K_OK;
+}
+
+}  // namespace
+
 extern "C" int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
                                   const float* a_scales, const float* b_scales, void* c, int c_dtype,
                                   const float* bias, const int32_t* bias_row_map, const void* residual,
@@ -85,4 +117,30 @@ extern "C" int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, i
     case M5K_F32: return launch_i8_splitk<M5K_F32>(a, b, m, n, k, p, splits, workspace, st, name);
     default: set_error("%s: unsupported output dtype %d", name, c_dtype); return M5K_EINVAL;
   }
+}
+
+extern "C" int m5k_gemm_i8_splitk_noalloc(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
+                                          const float* a_scales, const float* b_scales, void* c, int c_dtype,
+                                          const float* bias, const int32_t* bias_row_map, const void* residual,
+                                          const void* gate, const int32_t* gate_row_map, int splits, void* stream) {
+  clear_error();
+  const char* name = "m5k_gemm_i8_splitk_noalloc";
+  if (int rc = check_shape(m, n, k, name)) return rc;
+  M5K_REQUIRE(splits >= 1 && splits <= 64, "%s: splits=%d outside [1,64]", name, splits);
+  M5K_REQUIRE(static_cast<int64_t>(splits) * m * n <= M5K_SCRATCH_ELEMS,
+              "%s: splits*m*n = %lld INT32 partials exceed the %d-element scratch array", name,
+              (long long)(static_cast<int64_t>(splits) * m * n), M5K_SCRATCH_ELEMS);
+  int32_t* ws = nullptr;
+  if (int rc = scratch_of_current_device(&ws, name)) return rc;
+  // Every partial that the epilogue reads is written first by the split kernel, so the
+  // array needs no clearing between calls.
+  const int rc = m5k_gemm_i8_splitk(a, b, m, n, k, a_scales, b_scales, c, c_dtype, bias, bias_row_map, residual, gate,
+                                    gate_row_map, splits, ws, M5K_SCRATCH_ELEMS, stream);
+  if (rc != M5K_OK) {
+    // Report the failure under this entry point's name.
+    char detail[512];
+    snprintf(detail, sizeof(detail), "%s", m5k_last_error());
+    set_error("%s: %s", name, detail);
+  }
+  return rc;
 }
