@@ -260,6 +260,11 @@ def _qk_case(torch, dev, m=9914, k=4096, n=4096):
         return projection_qk_rope(q, wq, gamma, cos, sin, "int8", a_scales=s, b_scales=ws, epsilon=1e-6)
 
     t8 = time_op(torch, int8_online)
+    xq, xs = quantize(x, "int8")
+    fused = time_op(torch, lambda: projection_qk_rope(xq, wq, gamma, cos, sin, "int8", a_scales=xs, b_scales=ws,
+                                                      epsilon=1e-6))
+    staged = time_op(torch, lambda: qk_norm_rope(gemm(xq, wq, "int8", a_scales=xs, b_scales=ws,
+                                                      output_dtype=torch.bfloat16), gamma, cos, sin, epsilon=1e-6))
     tb = time_op(torch, lambda: projection_qk_rope(x, w, gamma, cos, sin, "bf16", epsilon=1e-6))
     proj = gemm(x, w, "bf16", output_dtype=bf)
     tpost = time_op(torch, lambda: qk_norm_rope(proj, gamma, cos, sin, epsilon=1e-6))
@@ -268,6 +273,9 @@ def _qk_case(torch, dev, m=9914, k=4096, n=4096):
         "m": m,
         "int8_online_ms": t8["avg_ms"],
         "int8_online_TOPS": ops / (t8["avg_ms"] * 1e-3) / 1e12,
+        "int8_fused_ms": fused["avg_ms"],
+        "int8_fused_TOPS": ops / (fused["avg_ms"] * 1e-3) / 1e12,
+        "int8_staged_gemm_plus_postprocess_ms": staged["avg_ms"],
         "bf16_fused_ms": tb["avg_ms"],
         "bf16_fused_TFLOPs": ops / (tb["avg_ms"] * 1e-3) / 1e12,
         "staged_postprocess_ms": tpost["avg_ms"],
@@ -519,21 +527,24 @@ def schedules_probe(torch, dev, rounds=6, reps=20):
 
 
 def settle(torch, fn, seconds):
-    """Run fn back to back for at least `seconds` of device time (synchronizing every 10 calls):
-    MI355X ramps its clocks over the first ~100 ms of sustained MFMA load after idle."""
+    """Run fn back to back for at least `seconds` of device time, synchronizing every 50 calls
+    and once at the end: MI355X ramps its clocks over the first ~100 ms of sustained MFMA load
+    after idle, and an idle gap of tens of milliseconds (as the first timing-event creation of
+    a process takes) drops them again, so the caller starts timing right after this returns."""
     t0, calls = time.perf_counter(), 0
     while time.perf_counter() - t0 < seconds:
-        for _ in range(10):
+        for _ in range(50):
             fn()
-        calls += 10
+        calls += 50
         torch.cuda.synchronize()
     return calls
 
 
 def counter_workload(torch, dev, reps):
     """The kernels whose hardware counters the profiles quote, `reps` launches each after a
-    clock-settling run, in this order: the FFN-down INT8 GEMM (ours), hipBLASLt's INT8 GEMM
-    (torch._int_mm) on the same codes, the FFN-down FP8 GEMM, the INT8 and FP8 quantizers on
+    clock-settling run, in this order: the FFN-down INT8 GEMM (ours), the same GEMM on constant
+    codes, hipBLASLt's INT8 GEMM (torch._int_mm) on the bench's codes, the FFN-down FP8 GEMM,
+    the INT8 and FP8 quantizers on
     the FFN-down activation, the fused gated and ungated prep (M 4096, K 4096, H128) and the
     RMS quantizer (M 4096, K 4096, H256).  For rocprofv3 --pmc runs; prints nothing else."""
     from m5kernels_amd import (fused_gated_residual_norm_hadamard_quantize, fused_norm_hadamard_quantize, gemm,
@@ -548,8 +559,12 @@ def counter_workload(torch, dev, reps):
     bf = torch.bfloat16
     ours = lambda: gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=bf)  # noqa: E731
     settle(torch, ours, 0.3)
+    # The same kernel on constant codes (every A and W code 1): identical instruction stream and
+    # memory traffic, with the MFMA array's data switching removed, to expose the power limit.
+    ones_a, ones_w = torch.ones_like(aq), torch.ones_like(wq)
     runs = [
         ("gemm_i8", ours),
+        ("gemm_i8_constant_codes", lambda: gemm(ones_a, ones_w, "int8", a_scales=sa, b_scales=ws, output_dtype=bf)),
         ("hipblaslt_int_mm", lambda: torch._int_mm(aq, wq_t)),
         ("gemm_f8", lambda: gemm(a8, w8, "fp8", a_scales=sa8, b_scales=ws8, output_dtype=bf)),
         ("quantize_int8", lambda: quantize(a, "int8")),
@@ -640,18 +655,15 @@ def main():
         aq, sa = quantize(a, "int8")
         return gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
 
-    log(f"[bench] warmup {args.warmup} steps, then at least {args.settle_seconds} s of steps")
+    steps = args.steps
+    # Timing events exist before the warmup: the first creation in a process costs tens of ms.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    log(f"[bench] warmup {args.warmup} steps, then at least {args.settle_seconds} s of steps; timing {steps} steps")
     for _ in range(args.warmup):
         y = step()
     torch.cuda.synchronize()
-    settle_steps = settle(torch, step, args.settle_seconds)
-    y = step()
-    torch.cuda.synchronize()
-
-    steps = args.steps
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    log(f"[bench] timing {steps} steps")
-    torch.cuda.synchronize()
+    settle_steps = settle(torch, step, args.settle_seconds)  # ends synchronized
     t0 = time.perf_counter()
     start.record()
     for i in range(steps):
@@ -662,7 +674,6 @@ def main():
     total_ms = start.elapsed_time(end)
     # Per-kernel durations: the same K steps again, an event pair around each kernel.
     log(f"[bench] per-kernel pass, {steps} steps")
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     for i in range(steps):
         ev[i][0].record()
         aq, sa = quantize(a, "int8")

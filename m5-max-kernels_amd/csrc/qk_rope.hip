@@ -190,21 +190,15 @@ __device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneR
   return make_uint4(packed[0], packed[1], packed[2], packed[3]);
 }
 
-template <int MODE, bool ALIGNED>
-__global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const uint8_t* __restrict__ A,
-                                                                          const uint8_t* __restrict__ B, int M, int N,
-                                                                          int64_t Kb, const float* __restrict__ sa,
-                                                                          const float* __restrict__ sb, QkParams p,
-                                                                          int fast) {
-  using G = KernelGrid;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  AccTile<MODE, G> acc;
-  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
-  else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
-
+// Epilogue of one 256 x G::TN projection tile (G::TN = 256: two heads, or 128: one head), called
+// by every thread after the main loop: the BF16 projection is staged in the LDS the loop has
+// released, then 16-lane groups normalize and rotate (row, head) pairs.
+template <int MODE, class G>
+__device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, int M, int N, int m0, int n0,
+                                                 const float* __restrict__ sa, const float* __restrict__ sb,
+                                                 const QkParams& p, int fast) {
+  static_assert(G::TN % HEAD == 0, "projection tiles hold whole heads");
+  constexpr int HPT = G::TN / HEAD;  // heads per tile
   // Everything the epilogue loads depends on the lane index taken here, after the main loop,
   // so no epilogue value is hoisted into the loop's register budget (with the interleaved
   // fragment reads the loop uses 241 of 256 VGPRs).
@@ -213,9 +207,9 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   const int group = tid_after >> 4, lg = tid_after & 15;
   constexpr int GROUPS = G::THREADS / 16;  // 32 groups of 16 lanes
   constexpr int ROWS_PER_GROUP = BM / GROUPS;
-  const int heads_here = (N - n0) >= BN ? 2 : 1;  // N is a multiple of 128
+  const int heads_here = min(G::TN, N - n0) / HEAD;  // N is a multiple of 128
 
-  // BF16 projection tile [256 rows][256 cols] in LDS (row stride TILE16_STRIDE).  The main
+  // BF16 projection tile [256 rows][G::TN cols] in LDS (row stride TILE16_STRIDE).  The main
   // loop ended with a drained DMA and a barrier, so the stage ring is free.
   uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
   for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
@@ -225,7 +219,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
     tile[(m - m0) * TILE16_STRIDE + (n - n0)] = static_cast<uint16_t>(f32_to_bf16_bits(value));
   });
   // Fast path: issue the per-row cos/sin loads of this group's rows once the accumulators are
-  // staged (their 64 registers are free then); the barrier below covers their latency.
+  // staged (their registers are free then); the barrier below covers their latency.
   LaneRope lr, lrk;  // Q (or single-projection) gamma; K gamma in the grouped layout
   uint4 cw[ROWS_PER_GROUP], sw[ROWS_PER_GROUP];
   int row0 = m0 + group;
@@ -249,7 +243,7 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
       const int row = m0 + local_row;
       if (row >= M) continue;  // uniform across the 16-lane group
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < HPT; ++h) {
         if (h >= heads_here) continue;
         const uint16_t* src = tile + local_row * TILE16_STRIDE + h * HEAD;
         const BlockDst d = block_dst(p, n0 / HEAD + h);  // uniform across the group
@@ -268,8 +262,8 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
     }
     return;
   }
-  for (int q = group; q < BM * 2; q += GROUPS) {
-    const int local_row = q >> 1, local_head = q & 1;
+  for (int q = group; q < BM * HPT; q += GROUPS) {
+    const int local_row = q / HPT, local_head = q % HPT;
     const int row = m0 + local_row;
     const int block = n0 / HEAD + local_head;
     if (row >= M || block * HEAD >= N) continue;  // uniform across the 16-lane group
@@ -286,6 +280,58 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
     float z[8];
     unpack8_bf16(*reinterpret_cast<const uint4*>(src + 8 * lg), z);
     norm_rope_16(z, [&](int dd) { return bf16_bits_to_f32(src[dd]); }, ps, row, M, d.head, lg);
+  }
+}
+
+template <int MODE, bool ALIGNED>
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const uint8_t* __restrict__ A,
+                                                                          const uint8_t* __restrict__ B, int M, int N,
+                                                                          int64_t Kb, const float* __restrict__ sa,
+                                                                          const float* __restrict__ sb, QkParams p,
+                                                                          int fast) {
+  using G = KernelGrid;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  AccTile<MODE, G> acc;
+  if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+  else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
+  qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, sa, sb, p, fast);
+}
+
+// The mixed schedule of the GEMM library (gemm_mixed_kernel) for the fused projection: the
+// first `full` tiles of the raster order (whole rounds) as 256 x 256 tiles, every other tile
+// as two 256 x 128 halves of one head each, so a partial last round runs as one shorter,
+// better-filled round.  Each output is one workgroup's dot product over all of K, so the bits
+// equal the plain launch's.
+template <int MODE>
+__global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_mixed_kernel(const uint8_t* __restrict__ A,
+                                                                          const uint8_t* __restrict__ B, int M, int N,
+                                                                          int64_t Kb, int full,
+                                                                          const float* __restrict__ sa,
+                                                                          const float* __restrict__ sb, QkParams p,
+                                                                          int fast) {
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int bid = static_cast<int>(blockIdx.x);
+  if (bid < full) {
+    using G = KernelGrid;
+    int tm, tn;
+    band_coords(xcd_logical(bid, full), tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    AccTile<MODE, G> acc;
+    mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+    qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, sa, sb, p, fast);
+  } else {
+    using G = gemm::detail::HalfGrid;
+    const int h = xcd_logical(bid - full, 2 * (tiles_m * tiles_n - full));
+    int tm, tn;
+    band_coords(full + (h >> 1), tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN + (h & 1) * G::TN;
+    if (n0 >= N) return;  // right half of a last tile column one head wide (whole workgroup)
+    AccTile<MODE, G> acc;
+    mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
+    qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, sa, sb, p, fast);
   }
 }
 
@@ -330,8 +376,20 @@ int launch_fused(const void* a, const void* b, int64_t m, int64_t n, int64_t k, 
   auto* A = static_cast<const uint8_t*>(a);
   auto* B = static_cast<const uint8_t*>(b);
   const int fast = fast_rope(p);
-  if (aligned) qk_fused_kernel<MODE, true><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p, fast);
-  else qk_fused_kernel<MODE, false><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p, fast);
+  if (aligned) {
+    // The GEMM library's schedule for this output shape; 256 x 224 tiles do not hold whole
+    // heads, so the narrow schedule is not offered here.
+    int64_t full = -1;
+    if (gemm::detail::plan_schedule(false, m, n, device_cus(), full) == gemm::detail::SCHED_MIXED) {
+      const int64_t wgs = full + 2 * (tiles - full);
+      qk_mixed_kernel<MODE><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(A, B, (int)m, (int)n, kb,
+                                                                               static_cast<int>(full), sa, sb, p, fast);
+    } else {
+      qk_fused_kernel<MODE, true><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p, fast);
+    }
+  } else {
+    qk_fused_kernel<MODE, false><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, sa, sb, p, fast);
+  }
   return launch_status("m5k_projection_qk_rope");
 }
 
