@@ -57,12 +57,11 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(const void* __re
 #pragma unroll
       for (int r = 0; r < EPC; ++r) v[i][r] = 0.0f;
     }
-    butterflies<B>(v[i]);
+    butterflies<B, false>(v[i]);
 #pragma unroll
     for (int r = 0; r < EPC; ++r) peak = fmaxf(peak, fabsf(v[i][r]));
   }
-  peak = block_max<kThreads / 64>(peak, red);
-  const I8Scale enc = i8_scale(quant_scale<M5K_QUANT_INT8>(peak));
+  const FoldedI8<B> enc(block_max<kThreads / 64>(peak, red));
   if (threadIdx.x == 0) scales[row] = enc.scale;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
@@ -75,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(const void* __re
 #pragma unroll
         for (int b = 0; b < 8; ++b) g[b] = v[i][8 * t + b];
         uint32_t w[2];
-        encode_i8<8>(g, enc, w);
+        enc.template encode<8>(g, w);
         out[t] = make_uint2(w[0], w[1]);
       }
     }

@@ -38,7 +38,9 @@ __device__ __forceinline__ constexpr float inv_sqrt_block() {
 }
 
 // In-place transform of v[EPC] for the calling lane (all lanes of a block must call).
-template <int B>
+// SCALED = false leaves out the final multiply by 1/sqrt(B); FoldedI8 applies it inside the
+// quantizer's encode instead.
+template <int B, bool SCALED = true>
 __device__ __forceinline__ void butterflies(float (&v)[Shape<B>::EPC]) {
   constexpr int EPC = Shape<B>::EPC, LPB = Shape<B>::LPB;
 #pragma unroll
@@ -62,10 +64,33 @@ __device__ __forceinline__ void butterflies(float (&v)[Shape<B>::EPC]) {
 #pragma unroll
     for (int r = 0; r < EPC; ++r) v[r] = __builtin_fmaf(sgn, v[r], __shfl_xor(v[r], m, 64));
   }
-  constexpr float inv = inv_sqrt_block<B>();
+  if constexpr (SCALED) {
+    constexpr float inv = inv_sqrt_block<B>();
 #pragma unroll
-  for (int r = 0; r < EPC; ++r) v[r] = v[r] * inv;
+    for (int r = 0; r < EPC; ++r) v[r] = v[r] * inv;
+  }
 }
+
+// Per-row INT8 encoder for butterflies<B, false> output z': the reference's rotated value is
+// z = fl(z' * c), c = 1/sqrt(B) in FP32, and its code clamp(rint(fl(z / scale))).  Rounding
+// is monotone, so the row peak max |z| = fl(max |z'| * c); the bracket multipliers come from
+// m~ = fl(c * fl(1 / scale)) (two roundings of c / scale) against the two-rounding chain.
+template <int B>
+struct FoldedI8 {
+  float scale;
+  I8Bracket bracket;
+  __device__ __forceinline__ explicit FoldedI8(float peak_unscaled) {
+    constexpr float c = inv_sqrt_block<B>();
+    const I8Scale s = i8_scale(quant_scale<M5K_QUANT_INT8>(peak_unscaled * c));
+    scale = s.scale;
+    bracket = i8_bracket(c * s.inv, s.exact);
+  }
+  template <int N>
+  __device__ __forceinline__ void encode(const float (&zu)[N], uint32_t (&out)[N / 4]) const {
+    const float sc = scale;
+    encode_i8<N>(zu, bracket, [sc](float z) { return i8_code_of((z * inv_sqrt_block<B>()) / sc); }, out);
+  }
+};
 
 // Load EPC consecutive elements of dtype DT starting at element index e (16-byte aligned
 // when the caller checked alignment) and apply the shared signs.

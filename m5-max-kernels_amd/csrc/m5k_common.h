@@ -167,31 +167,63 @@ __device__ __forceinline__ uint32_t i8_clamp_code(float r) {
   return static_cast<uint32_t>(static_cast<int>(c)) & 0xFFu;
 }
 
-// INT8 codes of N values (N % 4 == 0) packed 4 per word, bit-identical to
-// clamp(rint_even(fl(x / scale)), -127, 127) for every x of a row whose |x| <= peak.
-// Fast path: q0 = fl(x * inv).  With scale = fl(peak / 127), |x / scale| <= 127.01, and
-// |q0 - x/scale| <= 127.01 * (2^-23 + 2^-48) < 2^-16, so rint(q0) == rint(x/scale) unless a
-// rounding boundary n + 1/2 lies within 2^-16 of q0.  Clamping to [-127, 127] before the
-// rounding gives the same code.  Adding 1.5 * 2^23 rounds the clamped value to an integer
-// (round-half-even) and leaves its two's-complement low byte in the low byte of the sum's
-// bits.  If any element of the group lies within 2^-15 of a rounding boundary
-// (|qc - rint(qc)| >= 1/2 - 2^-15, exact ties included) the whole group takes the IEEE
-// division instead; one branch per group keeps the common path at about six VALU ops.
-template <int N>
-__device__ __forceinline__ void encode_i8(const float (&x)[N], const I8Scale& s, uint32_t (&out)[N / 4]) {
+// INT8 code of one value as the low byte of a word, from the row's exact chain:
+// clamp(rint_even(v), -127, 127) for the chain's FP32 result v.
+__device__ __forceinline__ uint32_t i8_code_of(float v) {
+  return i8_clamp_code(rintf(v));
+}
+
+// Row-constant INT8 encoder for codes clamp(rint_even(v(x)), -127, 127), where v(x) is the
+// row's chain of correctly rounded FP32 operations on x whose exact value is x * m for a row
+// constant m >= 0 (fl(x / scale): m = 1/scale; fl(fl(x * c) / scale): m = c/scale; ...).
+//
+// Fast path: t = fma(x, mult, 1.5 * 2^23) rounds x * mult to an integer once (the sum lies in
+// [2^23, 2^24), where the FP32 spacing is 1, and 1.5 * 2^23 is even, so ties go to the even
+// integer) and leaves its two's-complement low byte in the low byte of t's bits.  lo and hi
+// are 8 representable steps below and above m~, an FP32 estimate of m with at most two
+// roundings (|m~/m - 1| <= 2^-23 + 2^-48); 8 steps move m~ by more than 2^-21 (1 - 2^-20) of
+// itself, so lo <= m (1 - 2^-22) and hi >= m (1 + 2^-22).  A chain of at most three roundings
+// keeps v(x) / (x * m) within [1 - 3 * 2^-24, 1 + 3 * 2^-24 + 2^-46] of 1.  Then
+// x * lo <= v(x) <= x * hi (x >= 0; reversed for x < 0), and rounding to an integer is
+// monotone, so equal results of the two fused multiply-adds are rint(v(x)).  They are within
+// [-127, 127] whenever |x| <= the row peak the scale was derived from (|v| <= 127.0001), so
+// the clamp is inactive; m~ = 0 (an infinite scale, a zero peak) gives code 0 for every finite
+// x, as the chain does.  Otherwise (a half-integer between the two products, a NaN, or `exact`
+// set for a scale whose reciprocal is out of range) the call's N values take the chain itself,
+// on every lane of the wave.
+struct I8Bracket {
+  float lo, hi;
+  bool exact;  // every element takes the chain
+};
+
+// m_est is m~ (>= 0), exact forces the chain for the whole row.
+__device__ __forceinline__ I8Bracket i8_bracket(float m_est, bool exact) {
+  if (m_est == 0.0f) return I8Bracket{0.0f, 0.0f, exact};
+  const bool in_range = m_est >= 0x1p-100f && m_est <= 0x1p100f;
+  const uint32_t b = __float_as_uint(m_est);
+  return I8Bracket{__uint_as_float(b - 8u), __uint_as_float(b + 8u), exact || !in_range};
+}
+
+// N values (N % 4 == 0) to N INT8 codes packed 4 per word.  chain(x) returns the code of x
+// through the row's exact chain (a low byte), for groups the fast path cannot settle.
+template <int N, class Chain>
+__device__ __forceinline__ void encode_i8(const float (&x)[N], const I8Bracket& e, Chain chain,
+                                          uint32_t (&out)[N / 4]) {
   constexpr float kRound = 0x1.8p23f;
   uint32_t t[N];
-  float dev = s.exact ? 1.0f : 0.0f;
+  // Lanes whose products disagree (or are NaN), gathered as wave masks: one v_cmp per value and
+  // a scalar OR, instead of a per-lane boolean.  When any lane of the wave needs the chain, the
+  // whole wave takes it: on the other lanes it yields the fast path's codes again.
+  uint64_t unsettled = e.exact ? ~0ull : 0ull;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const float qc = fminf(fmaxf(x[i] * s.inv, -127.0f), 127.0f);
-    const float biased = qc + kRound;
-    dev = fmaxf(dev, fabsf(qc - (biased - kRound)));
-    t[i] = __float_as_uint(biased);
+    const float lo = __builtin_fmaf(x[i], e.lo, kRound), hi = __builtin_fmaf(x[i], e.hi, kRound);
+    unsettled |= __builtin_amdgcn_ballot_w64(!(lo == hi));
+    t[i] = __float_as_uint(hi);
   }
-  if (dev >= 0.5f - 0x1p-15f) {
+  if (unsettled) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) t[i] = __float_as_uint(fminf(fmaxf(rintf(x[i] / s.scale), -127.0f), 127.0f) + kRound);
+    for (int i = 0; i < N; ++i) t[i] = chain(x[i]);
   }
 #pragma unroll
   for (int w = 0; w < N / 4; ++w) {
@@ -201,6 +233,15 @@ __device__ __forceinline__ void encode_i8(const float (&x)[N], const I8Scale& s,
     const uint32_t hi = __builtin_amdgcn_perm(t[4 * w + 3], t[4 * w + 2], 0x04000C0Cu);
     out[w] = lo | hi;
   }
+}
+
+// The plain per-row quantizer's encoder: v(x) = fl(x / scale), m~ = fl(1 / scale).
+__device__ __forceinline__ I8Bracket i8_div_bracket(const I8Scale& s) { return i8_bracket(s.inv, s.exact); }
+
+template <int N>
+__device__ __forceinline__ void encode_i8_div(const float (&x)[N], const I8Scale& s, uint32_t (&out)[N / 4]) {
+  const float scale = s.scale;
+  encode_i8<N>(x, i8_div_bracket(s), [scale](float v) { return i8_code_of(v / scale); }, out);
 }
 
 // FP8 E4M3 codes of N values (N % 4 == 0) packed 4 per word, bit-identical to

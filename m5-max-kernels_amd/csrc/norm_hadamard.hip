@@ -19,9 +19,14 @@
 // Layout: one workgroup of 4 wave64 per row.  A lane owns NCH chunks of EPC consecutive
 // elements (chunk c = tid + 256*i) and the whole row stays in VGPRs: HBM traffic is the
 // minimum 2K (+2K branch, +2K R_next) + K + 4 bytes per row plus the parameter tables.  At
-// K = 4096 a lane holds 16 values, which keeps register use low enough for 8 resident
+// K = 4096 a lane holds 16 values, which keeps register use low enough for 7 resident
 // workgroups per CU; a one-wave-per-row layout (64 values per lane) measured slower for lack
-// of resident waves.
+// of resident waves.  So did variants that decode the column parameters once for several
+// rows (two rows per workgroup; or a contiguous range of rows per workgroup with the decoded
+// parameters held in VGPRs and the next row prefetched): they execute 10-20% fewer VALU
+// instructions per element but keep fewer rows' loads in flight per CU.
+#include <cmath>
+
 #include "hadamard_core.h"
 
 namespace m5k {
@@ -51,7 +56,15 @@ struct PrepParams {
   float eps;
   int layer;              // 1: LayerNorm, 0: RMS
   int round_input;        // 1: O = XDT, 0: O = FP32
+  float inv_k;            // 1/K when K is a power of two (exact), else 0
 };
+
+// sum / K for the row statistics: the IEEE quotient, or the same value as a multiply by the
+// exact reciprocal when K is a power of two.
+__device__ __forceinline__ float div_k(float x, const PrepParams& p) {
+  if (p.inv_k != 0.0f) return x * p.inv_k;
+  return x / static_cast<float>(p.k);
+}
 
 // Round 8 values through dtype DT in place (the O(...) / R(...) cast) and return their
 // storage words; BF16 pairs take one v_cvt_pk_bf16_f32 each.
@@ -119,9 +132,9 @@ __device__ __forceinline__ void load_input8(const PrepParams& p, int64_t row, in
 // layout's reduction (wave xor-butterfly; for GroupRow the 4 wave sums in order).  Chunks
 // past the row hold zeros and are re-zeroed after centring.
 template <class L, int NV>
-__device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV / 8], int64_t k, int layer,
-                                           float eps, float* red) {
-  const float kf = static_cast<float>(k);
+__device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV / 8], bool full,
+                                           const PrepParams& p, float* red) {
+  const int layer = p.layer;
   float first = 0.0f;
   if (layer) {
 #pragma unroll
@@ -130,24 +143,26 @@ __device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV
 #pragma unroll
     for (int i = 0; i < NV; ++i) first = __builtin_fmaf(v[i], v[i], first);
   }
-  first = L::sum(first, red) / kf;  // slot 0
+  first = div_k(L::sum(first, red), p);  // slot 0
   float var = first;
   if (layer) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] -= first;
+    if (!full) {  // uniform: only rows with lanes past the last chunk
 #pragma unroll
-    for (int c = 0; c < NV / 8; ++c) {
-      if (!live[c]) {
+      for (int c = 0; c < NV / 8; ++c) {
+        if (!live[c]) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) v[8 * c + r] = 0.0f;
+          for (int r = 0; r < 8; ++r) v[8 * c + r] = 0.0f;
+        }
       }
     }
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) acc = __builtin_fmaf(v[i], v[i], acc);
-    var = L::sum(acc, red + kWaves) / kf;  // slot 1
+    var = div_k(L::sum(acc, red + kWaves), p);  // slot 1
   }
-  return 1.0f / sqrtf(var + eps);
+  return 1.0f / sqrtf(var + p.eps);
 }
 
 // Raw 16-byte words of 8 elements of dtype DT (one word for 2-byte types, two for FP32).
@@ -186,48 +201,108 @@ __device__ __forceinline__ void decode8(const Raw8<DT>& r, float (&v)[8]) {
   }
 }
 
-// Fused kernel: NCH chunks of EPC elements per lane under layout L.  Every global load of
-// the row (X, branch, gate, gamma, scale, shift, signs) is issued up front, so a row waits
-// for memory once.  BDT is the branch dtype: XDT, or FP32 for a branch of another float dtype
-// (the host widens BF16/FP16 branches exactly), so float(branch) is the same value either way.
-template <class L, int XDT, int PDT, int B, int NCH, bool GATED, int BDT = XDT>
+// 8 elements at column `col` of a row whose base address is uniform (a 32-bit lane offset).
+template <int DT>
+__device__ __forceinline__ Raw8<DT> fetch8_at(const uint8_t* row_base, uint32_t col) {
+  const uint4* q = reinterpret_cast<const uint4*>(row_base + col * static_cast<uint32_t>(dtype_bytes<DT>()));
+  Raw8<DT> r;
+#pragma unroll
+  for (int i = 0; i < dtype_bytes<DT>() / 2; ++i) r.w[i] = q[i];
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void store_words8_at(uint8_t* row_base, uint32_t col,
+                                                const uint32_t (&w)[8 * dtype_bytes<DT>() / 4]) {
+  uint4* q = reinterpret_cast<uint4*>(row_base + col * static_cast<uint32_t>(dtype_bytes<DT>()));
+  q[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  if constexpr (DT == M5K_F32) q[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// Sign-bit masks of 8 columns for their parameter words (BF16 words hold elements 2i and 2i + 1
+// in bits 0-15 and 16-31; FP32 words one element each): XOR flips the sign of each column whose
+// int8 sign is negative.  v_perm_b32 moves sign bytes 2i and 2i + 1 to bytes 1 and 3 (selector
+// 0x0C yields zero), the AND keeps their top bits.
+template <int PDT>
+struct SignMask8 {
+  uint32_t m[PDT == M5K_F32 ? 8 : 4];
+  __device__ __forceinline__ explicit SignMask8(const uint2& s) {
+    if constexpr (PDT == M5K_F32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m[i] = ((i < 4 ? s.x : s.y) << (24 - 8 * (i & 3))) & 0x80000000u;
+    } else {
+      m[0] = __builtin_amdgcn_perm(0u, s.x, 0x010C000Cu) & 0x80008000u;
+      m[1] = __builtin_amdgcn_perm(0u, s.x, 0x030C020Cu) & 0x80008000u;
+      m[2] = __builtin_amdgcn_perm(0u, s.y, 0x010C000Cu) & 0x80008000u;
+      m[3] = __builtin_amdgcn_perm(0u, s.y, 0x030C020Cu) & 0x80008000u;
+    }
+  }
+  __device__ __forceinline__ Raw8<PDT> apply(Raw8<PDT> r) const {
+    if constexpr (PDT == M5K_F32) {
+      r.w[0].x ^= m[0]; r.w[0].y ^= m[1]; r.w[0].z ^= m[2]; r.w[0].w ^= m[3];
+      r.w[1].x ^= m[4]; r.w[1].y ^= m[5]; r.w[1].z ^= m[6]; r.w[1].w ^= m[7];
+    } else {
+      r.w[0].x ^= m[0]; r.w[0].y ^= m[1]; r.w[0].z ^= m[2]; r.w[0].w ^= m[3];
+    }
+    return r;
+  }
+};
+
+// Fused kernel: one row per workgroup of 4 wave64, NCH chunks of EPC elements per lane
+// (chunk c = tid + 256 i).  Every global load of the row (X, branch, gate, gamma, scale, shift,
+// signs) is issued up front, so a row waits for memory once.  BDT is the branch dtype: XDT, or
+// FP32 for a branch of another float dtype (the host widens BF16/FP16 branches exactly).
+//
+// The signs fold into gamma and shift as sign-bit flips of their words:
+// fma((c * inv) * (g * s), 1 + sc, sh * s) = s * fma((c * inv) * g, 1 + sc, sh) for s = +-1,
+// since negation commutes with every rounding (and with the O cast); only the sign of a zero
+// result can differ, and no code or scale depends on it (the butterflies, the row peak and the
+// encode treat +0 and -0 alike).  Signs are +-1 and enter as their sign bits.  The 1/sqrt(B)
+// multiply moves into the encode (FoldedI8).
+template <int XDT, int PDT, int B, int NCH, bool GATED, int BDT>
 __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int64_t rows) {
   __shared__ float red[3 * kWaves];  // one slot per block reduction
   constexpr int EPC = Shape<B>::EPC;
   constexpr int NV = NCH * EPC;
   constexpr int N8 = NV / 8;  // 8-element groups per lane
-  const int64_t row = L::row();
-  const int lane = L::lane();
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   const int64_t nchunks = p.k / EPC;
-  const int64_t goff = GATED && p.gate_map ? static_cast<int64_t>(p.gate_map[row]) * p.k : 0;
+  const bool full = nchunks == static_cast<int64_t>(NCH) * kThreads;
   const int64_t toff = p.row_map ? static_cast<int64_t>(p.row_map[row]) * p.k : 0;
+  const int64_t goff = GATED && p.gate_map ? static_cast<int64_t>(p.gate_map[row]) * p.k : 0;
+  uint32_t col[N8];  // first column of each 8-element group
   bool live[N8];
+#pragma unroll
+  for (int g = 0; g < N8; ++g) {
+    const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * kThreads;
+    col[g] = static_cast<uint32_t>(c * EPC + 8 * (g % (EPC / 8)));
+    live[g] = c < nchunks;
+  }
+  const uint8_t* xrow = static_cast<const uint8_t*>(p.x) + row * p.k * dtype_bytes<XDT>();
   Raw8<XDT> xr[N8];
   Raw8<BDT> br[GATED ? N8 : 1];
   Raw8<PDT> gr[GATED ? N8 : 1], gam[N8], scl[N8], shf[N8];
   uint2 sgn[N8];
 #pragma unroll
   for (int g = 0; g < N8; ++g) {
-    const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * L::kLanes;
-    const int64_t j = c * EPC + 8 * (g % (EPC / 8));
-    live[g] = c < nchunks;
     if (live[g]) {
-      xr[g] = fetch8<XDT>(p.x, row * p.k + j);
+      xr[g] = fetch8_at<XDT>(xrow, col[g]);
       if constexpr (GATED) {
-        br[g] = fetch8<BDT>(p.branch, row * p.k + j);
-        gr[g] = fetch8<PDT>(p.gate, goff + j);
+        br[g] = fetch8_at<BDT>(static_cast<const uint8_t*>(p.branch) + row * p.k * dtype_bytes<BDT>(), col[g]);
+        gr[g] = fetch8<PDT>(p.gate, goff + col[g]);
       }
-      gam[g] = fetch8<PDT>(p.gamma, j);
-      scl[g] = fetch8<PDT>(p.scale, toff + j);
-      shf[g] = fetch8<PDT>(p.shift, toff + j);
-      sgn[g] = *reinterpret_cast<const uint2*>(p.signs + j);
+      gam[g] = fetch8<PDT>(p.gamma, col[g]);
+      scl[g] = fetch8<PDT>(p.scale, toff + col[g]);
+      shf[g] = fetch8<PDT>(p.shift, toff + col[g]);
+      sgn[g] = *reinterpret_cast<const uint2*>(p.signs + col[g]);
     }
   }
+  // Row values: X, or the gated residual update (FP32 product, then add, one cast to the
+  // residual dtype, written once as R_next).
   float v[NV];
 #pragma unroll
   for (int g = 0; g < N8; ++g) {
-    const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * L::kLanes;
-    const int64_t j = c * EPC + 8 * (g % (EPC / 8));
     float t[8];
     if (live[g]) {
       decode8<XDT>(xr[g], t);
@@ -239,7 +314,7 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
         for (int i = 0; i < 8; ++i) t[i] = t[i] + b[i] * gt[i];
         uint32_t w[8 * dtype_bytes<XDT>() / 4];
         round8<XDT>(t, w);
-        store_words8<XDT>(p.r_next, row * p.k + j, w);
+        store_words8_at<XDT>(static_cast<uint8_t*>(p.r_next) + row * p.k * dtype_bytes<XDT>(), col[g], w);
       }
     } else {
 #pragma unroll
@@ -248,7 +323,9 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[8 * g + i] = t[i];
   }
-  const float inv = row_stats<L, NV>(v, live, p.k, p.layer, p.eps, red);
+  const float inv = row_stats<GroupRow, NV>(v, live, full, p, red);
+  // Modulation with the signs folded in, then the unscaled butterflies and the row peak:
+  // t = O(fma((c * inv) * gs, 1 + sc, hs)), gs and hs the sign-flipped gamma and shift.
   float peak = 0.0f;
 #pragma unroll
   for (int ci = 0; ci < NCH; ++ci) {
@@ -258,20 +335,16 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
       const int g = ci * (EPC / 8) + h;
       float t[8];
       if (live[g]) {
-        float gm[8], sc[8], sh[8];
-        decode8<PDT>(gam[g], gm);
+        const SignMask8<PDT> mask(sgn[g]);
+        float gs[8], sc[8], hs[8];
+        decode8<PDT>(mask.apply(gam[g]), gs);
         decode8<PDT>(scl[g], sc);
-        decode8<PDT>(shf[g], sh);
+        decode8<PDT>(mask.apply(shf[g]), hs);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = __builtin_fmaf(v[8 * g + i] * inv * gm[i], 1.0f + sc[i], sh[i]);
+        for (int i = 0; i < 8; ++i) t[i] = __builtin_fmaf(v[8 * g + i] * inv * gs[i], 1.0f + sc[i], hs[i]);
         if (p.round_input) {
           uint32_t w[8 * dtype_bytes<XDT>() / 4];
           round8<XDT>(t, w);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t byte = ((i < 4 ? sgn[g].x : sgn[g].y) >> (8 * (i & 3))) & 0xFFu;
-          t[i] = t[i] * static_cast<float>(static_cast<int8_t>(byte));
         }
       } else {
 #pragma unroll
@@ -280,27 +353,25 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
 #pragma unroll
       for (int i = 0; i < 8; ++i) z[8 * h + i] = t[i];
     }
-    hadamard::butterflies<B>(z);
+    hadamard::butterflies<B, false>(z);
 #pragma unroll
     for (int r = 0; r < EPC; ++r) {
       v[ci * EPC + r] = z[r];
       peak = fmaxf(peak, fabsf(z[r]));
     }
   }
-  peak = L::max(peak, red + 2 * kWaves);  // slot 2
-  const I8Scale enc = i8_scale(quant_scale<M5K_QUANT_INT8>(peak));
+  const hadamard::FoldedI8<B> enc(GroupRow::max(peak, red + 2 * kWaves));  // slot 2
   if (lane == 0) p.scales[row] = enc.scale;
+  int8_t* qrow = p.q + row * p.k;
 #pragma unroll
   for (int g = 0; g < N8; ++g) {
     if (live[g]) {
-      const int64_t c = lane + static_cast<int64_t>(g / (EPC / 8)) * L::kLanes;
-      const int64_t j = c * EPC + 8 * (g % (EPC / 8));
       float t[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) t[i] = v[8 * g + i];
       uint32_t w[2];
-      encode_i8<8>(t, enc, w);
-      *reinterpret_cast<uint2*>(p.q + row * p.k + j) = make_uint2(w[0], w[1]);
+      enc.template encode<8>(t, w);
+      *reinterpret_cast<uint2*>(qrow + col[g]) = make_uint2(w[0], w[1]);
     }
   }
 }
@@ -343,7 +414,7 @@ __global__ __launch_bounds__(kThreads) void norm_modulate_kernel(PrepParams p, i
 #pragma unroll
     for (int r = 0; r < 8; ++r) v[8 * i + r] = t[r];
   }
-  const float inv = row_stats<L, NV>(v, live, p.k, p.layer, p.eps, red);
+  const float inv = row_stats<L, NV>(v, live, nchunks == static_cast<int64_t>(NCH) * L::kLanes, p, red);
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int64_t c = lane + static_cast<int64_t>(i) * L::kLanes;
@@ -377,23 +448,24 @@ __global__ __launch_bounds__(kThreads) void gated_residual_kernel(PrepParams p, 
   load_input8<XDT, PDT, true, BDT>(p, row, goff, j, v);  // writes R_next
 }
 
+template <int XDT, int PDT, int B, int NCH, bool GATED, int BDT>
+int launch_prep(const PrepParams& p, int64_t rows, hipStream_t st) {
+  fused_prep_kernel<XDT, PDT, B, NCH, GATED, BDT><<<dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st>>>(p, rows);
+  return launch_status("m5k_norm_hadamard_quantize");
+}
+
 template <int XDT, int PDT, int B, bool GATED, int BDT>
 int launch_fused(const PrepParams& p, int64_t rows, hipStream_t st) {
   constexpr int EPC = Shape<B>::EPC;
-  const dim3 block(kThreads);
   const int64_t per_thread = (p.k / EPC + kThreads - 1) / kThreads;
-  const dim3 grid(static_cast<unsigned>(rows));
-  if (per_thread <= 1) fused_prep_kernel<GroupRow, XDT, PDT, B, 1, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 2) fused_prep_kernel<GroupRow, XDT, PDT, B, 2, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 3) fused_prep_kernel<GroupRow, XDT, PDT, B, 3, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 4) fused_prep_kernel<GroupRow, XDT, PDT, B, 4, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
-  else if (per_thread <= 8) fused_prep_kernel<GroupRow, XDT, PDT, B, 8, GATED, BDT><<<grid, block, 0, st>>>(p, rows);
-  else {
-    set_error("m5k_norm_hadamard_quantize: K=%lld exceeds the register-resident row limit %d", (long long)p.k,
-              8 * kThreads * EPC);
-    return M5K_EINVAL;
-  }
-  return launch_status("m5k_norm_hadamard_quantize");
+  if (per_thread <= 1) return launch_prep<XDT, PDT, B, 1, GATED, BDT>(p, rows, st);
+  if (per_thread <= 2) return launch_prep<XDT, PDT, B, 2, GATED, BDT>(p, rows, st);
+  if (per_thread <= 3) return launch_prep<XDT, PDT, B, 3, GATED, BDT>(p, rows, st);
+  if (per_thread <= 4) return launch_prep<XDT, PDT, B, 4, GATED, BDT>(p, rows, st);
+  if (per_thread <= 8) return launch_prep<XDT, PDT, B, 8, GATED, BDT>(p, rows, st);
+  set_error("m5k_norm_hadamard_quantize: K=%lld exceeds the register-resident row limit %d", (long long)p.k,
+            8 * kThreads * EPC);
+  return M5K_EINVAL;
 }
 
 template <int XDT, int PDT, bool GATED, int BDT = XDT>
@@ -472,6 +544,11 @@ int gate_by_branch(int pdt, int branch_dtype, const PrepParams& p, int64_t rows,
 
 bool a16(const void* ptr) { return ptr == nullptr || aligned16(ptr); }
 
+// 1/K for a power-of-two K (exactly representable), else 0.
+float exact_inv_k(int64_t k) {
+  return (k & (k - 1)) == 0 ? std::ldexp(1.0f, -__builtin_ctzll(static_cast<unsigned long long>(k))) : 0.0f;
+}
+
 int check_common(const void* x, int x_dtype, int64_t rows, int64_t k, int param_dtype, const char* name) {
   M5K_REQUIRE(x, "%s: null input", name);
   M5K_REQUIRE(rows > 0 && k > 0 && rows <= 0x7FFFFFFF, "%s: bad shape [%lld,%lld]", name, (long long)rows,
@@ -511,7 +588,7 @@ extern "C" int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t ro
                   (reinterpret_cast<uintptr_t>(signs) & 7u) == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0,
               "%s: misaligned buffers", name);
   PrepParams p{x,     branch, gate, gate_row_map, gamma,  scale, shift, row_map, signs, q, scales, residual_out,
-               nullptr, k, epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0};
+               nullptr, k, epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0, exact_inv_k(k)};
   hipStream_t st = as_stream(stream);
   switch (x_dtype) {
     case M5K_BF16: return fused_by_param<M5K_BF16>(param_dtype, block, branch_dtype, p, rows, st);
@@ -529,8 +606,8 @@ extern "C" int m5k_norm_modulate(const void* x, int x_dtype, int64_t rows, int64
   M5K_REQUIRE(gamma && scale && shift && y, "%s: null pointer", name);
   M5K_REQUIRE(epsilon > 0.0f, "%s: epsilon must be positive", name);
   M5K_REQUIRE(a16(x) && a16(gamma) && a16(scale) && a16(shift) && a16(y), "%s: misaligned buffers", name);
-  PrepParams p{x,       nullptr, nullptr, nullptr, gamma, scale, shift, row_map, nullptr, nullptr, nullptr, nullptr,
-               y,       k,       epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0};
+  PrepParams p{x, nullptr, nullptr, nullptr, gamma,   scale, shift, row_map, nullptr, nullptr, nullptr, nullptr,
+               y, k,       epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0, exact_inv_k(k)};
   hipStream_t st = as_stream(stream);
   switch (x_dtype) {
     case M5K_BF16: return norm_by_param<M5K_BF16>(param_dtype, p, rows, st);

@@ -5,8 +5,8 @@
 //   peak  = max |x|, NaN ignored           (FP32, order-independent => exact)
 //   scale = peak == 0 ? 1 : peak / 127     (or / 448 for FP8), IEEE division
 //   code  = clamp(rint_even(x / scale), -127, 127)   or  E4M3(x / scale)
-// INT8 codes come from a reciprocal multiply with a grouped exact fallback near rounding
-// boundaries (encode_i8), bit-identical to the IEEE division.
+// INT8 codes come from two fused multiply-adds that bracket the quotient, with a grouped
+// exact fallback near rounding boundaries (encode_i8), bit-identical to the IEEE division.
 //
 // A row is read once from HBM with 16-byte loads and held in VGPRs between the max
 // reduction and the encode, so HBM traffic is exactly 2*K (bf16 in) + K (codes out) + 4
@@ -91,7 +91,7 @@ __device__ __forceinline__ void encode_chunk(const uint4& v, const I8Scale& s, u
     }
   }
   uint32_t packed[EPC / 4];
-  if constexpr (MODE == M5K_QUANT_INT8) encode_i8<EPC>(f, s, packed);
+  if constexpr (MODE == M5K_QUANT_INT8) encode_i8_div<EPC>(f, s, packed);
   else encode_fp8<EPC>(f, s, packed);
   if constexpr (EPC == 8) *reinterpret_cast<uint2*>(out) = make_uint2(packed[0], packed[1]);
   else *reinterpret_cast<uint32_t*>(out) = packed[0];

@@ -114,26 +114,36 @@ __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) 
         for (int r = 0; r < 8; ++r) z[8 * h + r] = 0.0f;
       }
     }
-    hadamard::butterflies<B>(z);
+    hadamard::butterflies<B, false>(z);
 #pragma unroll
     for (int r = 0; r < EPC; ++r) {
       v[i * EPC + r] = z[r];
       peak = fmaxf(peak, fabsf(z[r]));
     }
   }
-  peak = block_max<kWaves>(peak, red + kWaves);
+  // The butterflies leave out the 1/sqrt(B) multiply: the reference's z is fl(z' * c), whose
+  // row peak is fl(max |z'| * c) (rounding is monotone), and its code
+  // rint(fl(fl(z / peak) * 127)), three roundings of z' * m for m = 127 c / peak, bracketed
+  // by the estimate m~ = fl(c * fl(127 / peak)) (two roundings; 0 for a zero or infinite peak,
+  // where every finite z codes to 0).
+  constexpr float c = hadamard::inv_sqrt_block<B>();
+  peak = block_max<kWaves>(peak, red + kWaves) * c;
   if constexpr (FOLD) inv = 1.0f / sqrtf(block_sum<kWaves>(ss, red + 2 * kWaves) / kf + p.eps);
   if (tid == 0) p.scales[row] = peak == 0.0f ? 1.0f : (FOLD ? peak * inv : peak) / 127.0f;
+  const I8Bracket enc = i8_bracket(peak == 0.0f ? 0.0f : c * (127.0f / peak), false);
+  const auto chain = [peak](float zu) { return rms_code(zu * c, peak); };
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     if (live[i]) {
-      const int64_t c = tid + static_cast<int64_t>(i) * kThreads;
+      const int64_t col = (tid + static_cast<int64_t>(i) * kThreads) * EPC;
 #pragma unroll
       for (int h = 0; h < EPC / 8; ++h) {
-        uint32_t w[2] = {0, 0};
+        float t[8];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) w[r >> 2] |= rms_code(v[i * EPC + 8 * h + r], peak) << (8 * (r & 3));
-        *reinterpret_cast<uint2*>(p.q + row * p.k + c * EPC + 8 * h) = make_uint2(w[0], w[1]);
+        for (int r = 0; r < 8; ++r) t[r] = v[i * EPC + 8 * h + r];
+        uint32_t w[2];
+        encode_i8<8>(t, enc, chain, w);
+        *reinterpret_cast<uint2*>(p.q + row * p.k + col + 8 * h) = make_uint2(w[0], w[1]);
       }
     }
   }

@@ -321,6 +321,48 @@ def test_gated_prep_mixed_branch_dtype_bit_exact(norm, dtype, branch_dtype, mapp
     assert torch.equal(gated_residual_add(rt, bt, gate, gate_row_map=gmap), upd)
 
 
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("dtype,block,width,round_output", [("bf16", 128, 4096, "input"), ("fp32", 32, 768, "input"),
+                                                            ("bf16", 1024, 4096, "fp32"), ("fp16", 64, 2048, "input"),
+                                                            ("bf16", 256, 5376, "input")])
+def test_irregular_table_maps_bit_exact(norm, gated, dtype, block, width, round_output, device):
+    """Three scale/shift tables and two gate tables in irregular row orders, a row with a
+    x40 outlier stripe and a constant row (LayerNorm centres it to zero); widths that fill
+    the lanes and widths that leave lanes idle.  Codes, scales and R_next equal the
+    fixed-order oracle bit for bit."""
+    rows = 23
+    rng = np.random.default_rng(width + block)
+    x = torch.from_numpy(rng.standard_normal((rows, width), dtype=np.float32)).to(device).to(DT[dtype])
+    x[5, ::61] *= 40
+    x[11] = 0.5  # a constant row: LayerNorm centres it to zero
+    gamma = (1 + 0.1 * torch.randn(width, device=device)).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(3, width, device=device)).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(3, width, device=device)).to(torch.bfloat16)
+    row_map = torch.tensor([0, 0, 1, 2, 2, 2, 0, 1, 1, 0, 2, 2, 2, 2, 1, 0, 0, 0, 1, 2, 0, 1, 1], dtype=torch.int32,
+                           device=device)
+    signs = torch.from_numpy(ref.hadamard_signs(width, 3)).to(device)
+    kw = {}
+    if gated:
+        kw = dict(branch=torch.from_numpy(rng.standard_normal((rows, width), dtype=np.float32)).to(device).to(DT[dtype]),
+                  gate=(0.3 * torch.randn(2, width, device=device)).to(torch.bfloat16),
+                  gate_row_map=torch.tensor([1, 0, 0, 0, 1, 1, 0, 1, 0, 0, 0, 1, 1, 1, 0, 0, 1, 1, 1, 0, 1, 0, 0],
+                                            dtype=torch.int32, device=device))
+        q, s, upd = fused_gated_residual_norm_hadamard_quantize(x, kw["branch"], kw["gate"], gamma, scale, shift, signs,
+                                                                block, norm=norm, round_output=round_output,
+                                                                gate_row_map=kw["gate_row_map"], row_map=row_map)
+        oq, os_, orn = _oracle_prep(x, gamma, scale, shift, signs, block, norm=norm, round_output=round_output,
+                                    row_map=row_map, **kw)
+        np.testing.assert_array_equal(upd.float().cpu().numpy(), orn)
+    else:
+        q, s = fused_norm_hadamard_quantize(x, gamma, scale, shift, signs, block, norm=norm, round_output=round_output,
+                                            row_map=row_map)
+        oq, os_ = _oracle_prep(x, gamma, scale, shift, signs, block, norm=norm, round_output=round_output,
+                               row_map=row_map)
+    np.testing.assert_array_equal(np_of(q), oq)
+    np.testing.assert_array_equal(np_of(s), os_)
+
+
 def test_gated_residual_add_mixed_dtype_through_c_abi(device):
     """m5k_gated_residual_add with an F32 branch beside a BF16 residual, called directly."""
     from m5kernels_amd import _lib
