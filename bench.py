@@ -90,6 +90,58 @@ def cpu_baseline(torch, a, wq, ws, y, target_s):
     }
 
 
+def numpy_baseline(torch, a, wq, ws, y, target_s):
+    """The reference's own validation idiom in NumPy on a bounded row sample: FP32 per-row
+    quantize, then the float64 product of the decoded codes (engine.py:173-175 of the
+    reference, there on sampled rows and columns).  W is decoded once, outside the timing, as
+    it is quantized offline."""
+    import numpy as np
+
+    from oracle import reference as ref
+
+    w_dec = ref.dequantize(wq.cpu().numpy(), ws.cpu().numpy(), "int8").astype(np.float64)
+
+    def step(rows):
+        q, s = ref.quantize_reference(a[:rows].float().cpu().numpy(), "int8")
+        return ref.dequantize(q, s, "int8").astype(np.float64) @ w_dec.T
+
+    probe_rows = 16
+    step(probe_rows)  # warm (thread pool)
+    t0 = time.perf_counter()
+    step(probe_rows)
+    per_row = (time.perf_counter() - t0) / probe_rows
+    rows = int(min(M, max(probe_rows, target_s / max(per_row, 1e-9))))
+    a_host = a[:rows].float().cpu()  # the device-to-host copy stays outside the timing
+    t0 = time.perf_counter()
+    q, s = ref.quantize_reference(a_host.numpy(), "int8")
+    out = ref.dequantize(q, s, "int8").astype(np.float64) @ w_dec.T
+    elapsed = time.perf_counter() - t0
+    gpu = y[:rows].float().cpu().numpy().astype(np.float64)
+    rel = float(np.linalg.norm(gpu - out) / np.linalg.norm(out))
+    return {
+        "value": 2.0 * rows * N * K / elapsed / 1e12,
+        "unit": "TOPS",
+        "cores": len(os.sched_getaffinity(0)),
+        "threads_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")},
+        "sample": f"rows 0..{rows - 1} of the {M}-row FFN-down step: NumPy FP32 per-row INT8 quantize + float64 "
+        f"matmul of the decoded codes against the decoded W [{N},{K}]",
+        "seconds": elapsed,
+        "ms_per_full_step_extrapolated": elapsed / rows * M * 1e3,
+        "relative_l2_vs_gpu_bf16_rows": rel,
+    }
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def time_op(torch, fn, reps=20, warm=10):
     """Device time of fn on the current stream.
 
@@ -816,6 +868,9 @@ def main():
     if not args.no_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, a, wq, ws, y, args.cpu_seconds)
+        result["cpu_baseline"]["cpu_model"] = cpu_model()
+        log("[bench] cpu baseline, NumPy variant")
+        result["cpu_baseline"]["numpy_variant"] = numpy_baseline(torch, a, wq, ws, y, args.cpu_seconds / 2)
 
     print(json.dumps(result), flush=True)
 

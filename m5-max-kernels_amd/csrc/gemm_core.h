@@ -175,10 +175,12 @@ constexpr int TILE16_STRIDE = BN + 8;
 
 // All LDS of a GEMM kernel: NST stages x (A, B) x 32 KiB = 128 KiB for the main loop, which uses
 // it as the stage ring; epilogues may reuse it afterwards (a 256 x TILE16_STRIDE 16-bit tile,
-// 132 KiB).  The DMA writes are inline asm with "memory" clobbers and every consumer sits
-// behind an explicit wait and barrier, so one array serves all stages.
-constexpr int LDS_BYTES = NST * 2 * STAGE_BYTES > BM * TILE16_STRIDE * 2 ? NST * 2 * STAGE_BYTES
-                                                                         : BM * TILE16_STRIDE * 2;
+// 132 KiB, then the tile's row and column scales, 2 KiB).  The DMA writes are inline asm with
+// "memory" clobbers and every consumer sits behind an explicit wait and barrier, so one array
+// serves all stages.
+constexpr int EPI_SCALES_OFFSET = BM * TILE16_STRIDE * 2;
+constexpr int EPI_BYTES = EPI_SCALES_OFFSET + (BM + BN) * 4;
+constexpr int LDS_BYTES = NST * 2 * STAGE_BYTES > EPI_BYTES ? NST * 2 * STAGE_BYTES : EPI_BYTES;
 __shared__ __attribute__((aligned(16))) uint8_t g_lds[LDS_BYTES];
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -541,6 +543,56 @@ __device__ __forceinline__ void mainloop_staged(const uint8_t* __restrict__ A, c
     __syncthreads();
   }
 }
+
+// Lane geometry of an accumulator tile: element e of block (i, j) lies at tile row row(i, e) and
+// tile column col(j).  16 x 16 blocks: lane l holds column l & 15, rows 4 (l >> 4) + e;
+// 32 x 32 blocks: column l & 31, rows 8 (e >> 2) + 4 (l >> 5) + (e & 3).
+// The lane index comes from an opaque copy of threadIdx.x taken after the main loop: loads that
+// depend on it (scales, bias) then stay after the loop instead of being hoisted into its
+// register budget (the 16 x 16 main loop uses 241 of 256 VGPRs).
+__device__ __forceinline__ int tid_after_mainloop() {
+  int t = threadIdx.x;
+  __asm__ volatile("" : "+v"(t));
+  return t;
+}
+
+template <int MODE, class G>
+struct AccGeom {
+  static constexpr int MD = Blk<MODE, G>::MD, FM = Blk<MODE, G>::FM, FN = Blk<MODE, G>::FN;
+  static constexpr int PER = MD == 32 ? 16 : 4;  // elements per block and lane
+  int r0, c0;
+  __device__ __forceinline__ explicit AccGeom(int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+    r0 = wm * G::WM + (lane >> (MD == 32 ? 5 : 4)) * 4;
+    c0 = wn * G::WN + (lane & (MD - 1));
+  }
+  __device__ __forceinline__ int row(int i, int e) const {
+    return r0 + i * MD + (MD == 32 ? (e >> 2) * 8 + (e & 3) : e);
+  }
+  __device__ __forceinline__ int col(int j) const { return c0 + j * MD; }
+};
+
+// Row and column scales of a tile, staged in the LDS after the 16-bit tile by one coalesced
+// load per thread (0 past the matrix; every thread of the workgroup calls it after the main
+// loop, whose last barrier freed the LDS).  Lanes then read their scales from the LDS one
+// block row at a time, so the epilogue waits for HBM once and holds few extra registers.
+template <class G>
+struct TileScales {
+  const float* s;  // rows [0, BM), then columns [BM, BM + G::TN)
+  __device__ __forceinline__ TileScales(const float* __restrict__ sa, const float* __restrict__ sb, int M, int N,
+                                        int m0, int n0, int tid) {
+    float* w = reinterpret_cast<float*>(g_lds + EPI_SCALES_OFFSET);
+    for (int t = tid; t < BM + G::TN; t += G::THREADS) {
+      const int m = m0 + t, n = n0 + t - BM;
+      w[t] = t < BM ? (m < M ? sa[m] : 0.0f) : (n < N ? sb[n] : 0.0f);
+    }
+    __syncthreads();
+    s = w;
+  }
+  __device__ __forceinline__ float row(int r) const { return s[r]; }
+  __device__ __forceinline__ float col(int c) const { return s[BM + c]; }
+};
 
 // Visit every accumulator element with its global (row, col).
 template <class G, class AccT, int FM, int FN, class F>

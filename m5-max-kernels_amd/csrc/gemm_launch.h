@@ -38,85 +38,167 @@ struct EpiParams {
 using KernelGrid = Grid8;
 
 // Scale epilogue of one 256 x G::TN tile (every thread of the workgroup calls it; the LDS is
-// free).  RAW writes the INT32 accumulators.
+// free).  RAW writes the INT32 accumulators.  The per-row and per-column operands of the
+// lane's elements (scales, bias vector) are loaded in one batch before the arithmetic, and a
+// bias table's offsets and values one block row at a time, so the epilogue waits for memory a
+// few times instead of once per element.
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW, class G = KernelGrid>
 __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int N, int m0, int n0,
                                          const EpiParams& p) {
-  auto scaled = [&](int m, int n, auto v) {
-    float value;
-    if constexpr (MODE == I8 || MODE == F8) value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
-    else value = v;
-    if constexpr (BIAS != EPI_NONE) {
-      const int64_t boff = BIAS == EPI_TABLE ? (int64_t)p.bias_map[m] * N : 0;
-      value = value + p.bias[boff + n];
-    }
-    return value;
-  };
-
-  // 16-bit outputs: stage the rounded tile (the BF16 branch for the gated form) in the LDS the
-  // main loop has released, then write whole 512-byte tile rows with 16-byte stores.
-  if constexpr (!RAW && (OUT_DT == M5K_BF16 || OUT_DT == M5K_F16)) {
-    if (p.coalesced) {
-      uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
-      for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
-        const float value = (m < M && n < N) ? scaled(m, n, v) : 0.0f;
-        tile[(m - m0) * TILE16_STRIDE + (n - n0)] = static_cast<uint16_t>(
-            GATE != EPI_NONE || OUT_DT == M5K_BF16 ? f32_to_bf16_bits(value) : f32_to_f16_bits(value));
-      });
-      __syncthreads();
-      constexpr int CPR = G::TN / 8;  // 16-byte chunks per tile row
-      for (int c = threadIdx.x; c < BM * CPR; c += G::THREADS) {
-        const int r = c / CPR, cc = c % CPR;
-        const int m = m0 + r, n = n0 + 8 * cc;
-        if (m >= M || n >= N) continue;  // N % 8 == 0: a chunk is wholly in or out
-        uint4 w = *reinterpret_cast<const uint4*>(tile + r * TILE16_STRIDE + 8 * cc);
-        const int64_t idx = (int64_t)m * N + n;
-        if constexpr (GATE != EPI_NONE) {
-          const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;
-          const uint4 rw = *reinterpret_cast<const uint4*>(p.residual + idx);
-          const uint4 gw = *reinterpret_cast<const uint4*>(p.gate + goff + n);
-          const uint32_t bs[4] = {w.x, w.y, w.z, w.w}, rs[4] = {rw.x, rw.y, rw.z, rw.w},
-                         gs[4] = {gw.x, gw.y, gw.z, gw.w};
-          uint32_t out[4];
+  using Geo = AccGeom<MODE, G>;
+  constexpr bool QUANT = MODE == I8 || MODE == F8;
+  const int tid = tid_after_mainloop();
+  const Geo geo(tid);
+  if constexpr (RAW) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float lo = bf16_bits_to_f32(rs[t] & 0xFFFFu) +
-                             bf16_bits_to_f32(bs[t] & 0xFFFFu) * bf16_bits_to_f32(gs[t] & 0xFFFFu);
-            const float hi = bf16_bits_to_f32(rs[t] >> 16) + bf16_bits_to_f32(bs[t] >> 16) * bf16_bits_to_f32(gs[t] >> 16);
-            out[t] = f32x2_to_bf16x2(lo, hi);
-          }
-          w = make_uint4(out[0], out[1], out[2], out[3]);
+    for (int i = 0; i < Geo::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) {
+          const int m = m0 + geo.row(i, e), n = n0 + geo.col(j);
+          if (m < M && n < N) static_cast<int32_t*>(p.c)[(int64_t)m * N + n] = acc[i][j][e];
         }
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + idx) = w;
+    return;
+  } else {
+    float cs[QUANT ? Geo::FN : 1];
+    const float* sc = nullptr;
+    if constexpr (QUANT) {
+      const TileScales<G> ts(p.sa, p.sb, M, N, m0, n0, tid);
+      sc = ts.s;
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j) cs[j] = ts.col(geo.col(j));
+    }
+    float bvec[BIAS == EPI_VECTOR ? Geo::FN : 1];
+    if constexpr (BIAS == EPI_VECTOR) {
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j) {
+        const int n = n0 + geo.col(j);
+        bvec[j] = n < N ? p.bias[n] : 0.0f;
       }
-      return;
+    }
+    // FP32 value of block row i's elements: the scale epilogue, then the bias (a bias table's
+    // row offsets and values are loaded per block row, two batches).
+    auto row_values = [&](int i, float (&val)[Geo::FN][Geo::PER]) {
+      float rs[QUANT ? Geo::PER : 1];
+      if constexpr (QUANT) {
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) rs[e] = sc[geo.row(i, e)];
+      }
+      float tb[BIAS == EPI_TABLE ? Geo::FN : 1][BIAS == EPI_TABLE ? Geo::PER : 1];
+      if constexpr (BIAS == EPI_TABLE) {
+        int64_t brow[Geo::PER];
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) {
+          const int m = m0 + geo.row(i, e);
+          brow[e] = m < M ? (int64_t)p.bias_map[m] * N : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+          for (int e = 0; e < Geo::PER; ++e) {
+            const int m = m0 + geo.row(i, e), n = n0 + geo.col(j);
+            tb[j][e] = (m < M && n < N) ? p.bias[brow[e] + n] : 0.0f;
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) {
+          float value;
+          if constexpr (QUANT) value = (static_cast<float>(acc[i][j][e]) * rs[e]) * cs[j];
+          else value = acc[i][j][e];
+          if constexpr (BIAS == EPI_VECTOR) value = value + bvec[j];
+          if constexpr (BIAS == EPI_TABLE) value = value + tb[j][e];
+          val[j][e] = value;
+        }
+    };
+
+    // 16-bit outputs: stage the rounded tile (the BF16 branch for the gated form) in the LDS the
+    // main loop has released, then write whole 512-byte tile rows with 16-byte stores.
+    if constexpr (OUT_DT == M5K_BF16 || OUT_DT == M5K_F16) {
+      if (p.coalesced) {
+        uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
+#pragma unroll
+        for (int i = 0; i < Geo::FM; ++i) {
+          float val[Geo::FN][Geo::PER];
+          row_values(i, val);
+#pragma unroll
+          for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+            for (int e = 0; e < Geo::PER; ++e) {
+              const int r = geo.row(i, e), c = geo.col(j);
+              const float value = (m0 + r < M && n0 + c < N) ? val[j][e] : 0.0f;
+              tile[r * TILE16_STRIDE + c] = static_cast<uint16_t>(
+                  GATE != EPI_NONE || OUT_DT == M5K_BF16 ? f32_to_bf16_bits(value) : f32_to_f16_bits(value));
+            }
+        }
+        __syncthreads();
+        constexpr int CPR = G::TN / 8;  // 16-byte chunks per tile row
+        for (int c = threadIdx.x; c < BM * CPR; c += G::THREADS) {
+          const int r = c / CPR, cc = c % CPR;
+          const int m = m0 + r, n = n0 + 8 * cc;
+          if (m >= M || n >= N) continue;  // N % 8 == 0: a chunk is wholly in or out
+          uint4 w = *reinterpret_cast<const uint4*>(tile + r * TILE16_STRIDE + 8 * cc);
+          const int64_t idx = (int64_t)m * N + n;
+          if constexpr (GATE != EPI_NONE) {
+            const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;
+            const uint4 rw = *reinterpret_cast<const uint4*>(p.residual + idx);
+            const uint4 gw = *reinterpret_cast<const uint4*>(p.gate + goff + n);
+            const uint32_t bs[4] = {w.x, w.y, w.z, w.w}, rs[4] = {rw.x, rw.y, rw.z, rw.w},
+                           gs[4] = {gw.x, gw.y, gw.z, gw.w};
+            uint32_t out[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float lo = bf16_bits_to_f32(rs[t] & 0xFFFFu) +
+                               bf16_bits_to_f32(bs[t] & 0xFFFFu) * bf16_bits_to_f32(gs[t] & 0xFFFFu);
+              const float hi =
+                  bf16_bits_to_f32(rs[t] >> 16) + bf16_bits_to_f32(bs[t] >> 16) * bf16_bits_to_f32(gs[t] >> 16);
+              out[t] = f32x2_to_bf16x2(lo, hi);
+            }
+            w = make_uint4(out[0], out[1], out[2], out[3]);
+          }
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + idx) = w;
+        }
+        return;
+      }
+    }
+
+#pragma unroll
+    for (int i = 0; i < Geo::FM; ++i) {
+      float val[Geo::FN][Geo::PER];
+      row_values(i, val);
+      // The gated form's residual and gate values of this block row, loaded in one batch.
+      float res[GATE != EPI_NONE ? Geo::FN : 1][GATE != EPI_NONE ? Geo::PER : 1];
+      float gte[GATE != EPI_NONE ? Geo::FN : 1][GATE != EPI_NONE ? Geo::PER : 1];
+      if constexpr (GATE != EPI_NONE) {
+#pragma unroll
+        for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+          for (int e = 0; e < Geo::PER; ++e) {
+            const int m = m0 + geo.row(i, e), n = n0 + geo.col(j);
+            const bool in = m < M && n < N;
+            const int64_t goff = GATE == EPI_TABLE && in ? (int64_t)p.gate_map[m] * N : 0;
+            res[j][e] = in ? bf16_bits_to_f32(p.residual[(int64_t)m * N + n]) : 0.0f;
+            gte[j][e] = in ? bf16_bits_to_f32(p.gate[goff + n]) : 0.0f;
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) {
+          const int m = m0 + geo.row(i, e), n = n0 + geo.col(j);
+          if (m >= M || n >= N) continue;
+          const int64_t idx = (int64_t)m * N + n;
+          if constexpr (GATE != EPI_NONE) {
+            const float branch = round_through<M5K_BF16>(val[j][e]);
+            store_elem<M5K_BF16>(p.c, idx, res[j][e] + branch * gte[j][e]);
+          } else {
+            store_elem<OUT_DT>(p.c, idx, val[j][e]);
+          }
+        }
     }
   }
-
-  for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
-    if (m >= M || n >= N) return;
-    const int64_t idx = (int64_t)m * N + n;
-    if constexpr (RAW) {
-      static_cast<int32_t*>(p.c)[idx] = v;
-    } else {
-      float value;
-      if constexpr (MODE == I8 || MODE == F8) value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
-      else value = v;
-      if constexpr (BIAS != EPI_NONE) {
-        const int64_t boff = BIAS == EPI_TABLE ? (int64_t)p.bias_map[m] * N : 0;
-        value = value + p.bias[boff + n];
-      }
-      if constexpr (GATE != EPI_NONE) {
-        const int64_t goff = GATE == EPI_TABLE ? (int64_t)p.gate_map[m] * N : 0;
-        const float branch = round_through<M5K_BF16>(value);
-        const float res = bf16_bits_to_f32(p.residual[idx]);
-        const float g = bf16_bits_to_f32(p.gate[goff + n]);
-        store_elem<M5K_BF16>(p.c, idx, res + branch * g);
-      } else {
-        store_elem<OUT_DT>(p.c, idx, value);
-      }
-    }
-  });
 }
 
 // One 256 x G::TN output tile per workgroup.

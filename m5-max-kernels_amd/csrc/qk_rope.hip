@@ -212,12 +212,36 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
   // BF16 projection tile [256 rows][G::TN cols] in LDS (row stride TILE16_STRIDE).  The main
   // loop ended with a drained DMA and a barrier, so the stage ring is free.
   uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
-  for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
-    float value;
-    if constexpr (MODE == I8) value = (m < M && n < N) ? (static_cast<float>(v) * sa[m]) * sb[n] : 0.0f;
-    else value = v;
-    tile[(m - m0) * TILE16_STRIDE + (n - n0)] = static_cast<uint16_t>(f32_to_bf16_bits(value));
-  });
+  {
+    using Geo = AccGeom<MODE, G>;
+    const Geo geo(tid_after);
+    float cs[Geo::FN];
+    const float* sc = nullptr;
+    if constexpr (MODE == I8) {
+      const TileScales<G> ts(sa, sb, M, N, m0, n0, tid_after);
+      sc = ts.s;
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j) cs[j] = ts.col(geo.col(j));
+    }
+#pragma unroll
+    for (int i = 0; i < Geo::FM; ++i) {
+      float rs[Geo::PER];
+      if constexpr (MODE == I8) {
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) rs[e] = sc[geo.row(i, e)];
+      }
+#pragma unroll
+      for (int j = 0; j < Geo::FN; ++j)
+#pragma unroll
+        for (int e = 0; e < Geo::PER; ++e) {
+          const int r = geo.row(i, e), c = geo.col(j);
+          float value;
+          if constexpr (MODE == I8) value = (m0 + r < M && n0 + c < N) ? (static_cast<float>(acc[i][j][e]) * rs[e]) * cs[j] : 0.0f;
+          else value = acc[i][j][e];
+          tile[r * TILE16_STRIDE + c] = static_cast<uint16_t>(f32_to_bf16_bits(value));
+        }
+    }
+  }
   // Fast path: issue the per-row cos/sin loads of this group's rows once the accumulators are
   // staged (their registers are free then); the barrier below covers their latency.
   LaneRope lr, lrk;  // Q (or single-projection) gamma; K gamma in the grouped layout
