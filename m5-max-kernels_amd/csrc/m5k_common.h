@@ -245,38 +245,30 @@ __device__ __forceinline__ void encode_i8_div(const float (&x)[N], const I8Scale
 }
 
 // FP8 E4M3 codes of N values (N % 4 == 0) packed 4 per word, bit-identical to
-// fp8_e4m3_encode(fl(x / scale)) for every x of a row whose |x| <= peak, scale = fl(peak / 448).
-// Fast path: y = fl(x * inv) clamped to [-448, 448] and converted by v_cvt_pk_fp8_f32, which
-// equals fp8_e4m3_encode on every finite f32 of magnitude below 464 (all 2.28e9 of them
-// compared on MI355X) and rounds monotonically in the magnitude.  y and fl(x / scale) differ by
-// at most 3 ulp(y) (the reciprocal and the product each round once), i.e. at most 6 ulps of
-// the binade below; so when the magnitudes 8 ulps below and above |y| convert to the same code,
-// fl(x / scale) converts to that code too.  Otherwise the group takes the IEEE division and the
-// software encoder.
+// fp8_e4m3_encode(fl(x / scale)) for every finite x of a row whose |x| <= peak,
+// scale = fl(peak / 448).  The products fl(x * lo) and fl(x * hi), with lo and hi the
+// multipliers of i8_bracket(fl(1 / scale)), bracket fl(x / scale): the multipliers sit more than
+// 2^-22 of 1/scale away from it, each product and the quotient round once (2^-24).
+// v_cvt_pk_fp8_f32 equals fp8_e4m3_encode on every finite f32 of magnitude below 464 (all
+// 2.28e9 of them compared on MI355X; |x * hi| <= 448.001 here) and is monotone in the value, so
+// when both products give the same code, fl(x / scale) gives it too.  Otherwise (or for an
+// out-of-range reciprocal) the call's values take the IEEE division and the software encoder,
+// on every lane of the wave.  A NaN input has no defined code.
 template <int N>
 __device__ __forceinline__ void encode_fp8(const float (&x)[N], const I8Scale& s, uint32_t (&out)[N / 4]) {
-  bool ok = !s.exact;
+  const I8Bracket e = i8_bracket(s.inv, s.exact);
+  uint64_t unsettled = e.exact ? ~0ull : 0ull;
 #pragma unroll
   for (int w = 0; w < N / 4; ++w) {
-    float y[4], below[4], above[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      y[b] = fminf(fmaxf(x[4 * w + b] * s.inv, -448.0f), 448.0f);
-      const uint32_t a = __float_as_uint(y[b]) & 0x7FFFFFFFu;
-      below[b] = __uint_as_float(a > 8u ? a - 8u : 0u);
-      above[b] = __uint_as_float(a + 8u);
-    }
     // word_sel false writes bits [15:0] (first operand in the low byte), true bits [31:16].
-    int word = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-    word = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], word, true);
-    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(below[0], below[1], 0, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(below[2], below[3], lo, true);
-    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(above[0], above[1], 0, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(above[2], above[3], hi, true);
-    ok = ok && lo == hi;
-    out[w] = static_cast<uint32_t>(word);
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w] * e.lo, x[4 * w + 1] * e.lo, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * e.lo, x[4 * w + 3] * e.lo, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w] * e.hi, x[4 * w + 1] * e.hi, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * e.hi, x[4 * w + 3] * e.hi, hi, true);
+    unsettled |= __builtin_amdgcn_ballot_w64(lo != hi);
+    out[w] = static_cast<uint32_t>(hi);
   }
-  if (!ok) {
+  if (unsettled) {
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
       uint32_t word = 0;
