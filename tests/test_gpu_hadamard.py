@@ -88,3 +88,22 @@ def test_strided_input_not_mutated(device):
     y = rotate(view, 256, signs)
     np.testing.assert_array_equal(np_of(y), ref.c_hadamard_f32(view.cpu().numpy(), 256, np.ones(512, np.int8)))
     assert torch.equal(base, before)
+
+
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_rotate_quantize_extreme_rows_bit_exact(block, device):
+    """The folded 1/sqrt(B) encoder on rows far from unit scale: peaks that put the reciprocal
+    scale outside the fast range (the whole row takes the exact chain), a zero row, and an
+    ordinary row.  Codes and scales equal quantize(c_hadamard_f32(x)) bit for bit."""
+    rng = np.random.default_rng(block)
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    x[0] *= np.float32(1e-33)
+    x[1] *= np.float32(1e35)
+    x[2] = 0.0
+    x[3] *= np.float32(1e-30)
+    xt = torch.from_numpy(x).to(device)
+    signs = torch.from_numpy(ref.hadamard_signs(2048, 3)).to(device)
+    q, s = rotate_quantize(xt, block, signs)
+    rq, rs = ref.quantize_reference(ref.c_hadamard_f32(x, block, np_of(signs)), "int8")
+    np.testing.assert_array_equal(np_of(q), rq)
+    np.testing.assert_array_equal(np_of(s), rs)

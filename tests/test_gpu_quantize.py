@@ -129,6 +129,30 @@ def test_nan_ignored_by_row_peak(dtype, device):
     np.testing.assert_array_equal(np_of(q)[finite], rq[finite])
 
 
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_extreme_row_scales_bit_exact(mode, dtype, device):
+    """Rows whose reciprocal scale leaves the encoder's fast range (peak ~1e-33: scale below
+    2^-100; peak ~1e37: reciprocal below 2^-100) take the exact chain for the whole row; a
+    row holding +-inf has an infinite scale and codes 0 for its finite elements, as the IEEE
+    division gives.  Finite elements' codes and every scale bit-exact against the oracle."""
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((6, 4096)).astype(np.float32)
+    x[0] *= np.float32(1e-33)
+    x[1] *= np.float32(1e-35)
+    x[2] *= np.float32(1e37)
+    x[3, 100] = np.inf
+    x[4, 7] = -np.inf
+    x[5] *= np.float32(2.5e-29)  # scale near 2^-100, the switch to the exact chain
+    xt = torch.from_numpy(x).to(device).to(DTYPES[dtype])
+    q, s = quantize(xt, mode)
+    x32 = xt.float().cpu().numpy()
+    rq, rs = ref.c_quantize_rows(x32, mode)
+    np.testing.assert_array_equal(np_of(s), rs)
+    finite = np.isfinite(x32)
+    np.testing.assert_array_equal(np_of(q)[finite], rq[finite])
+
+
 def test_round_half_even_kat(kats, device):
     kat = kats["int8_round_half_even"]
     x = torch.tensor([kat["row"]] * 3, dtype=torch.float32, device=device)

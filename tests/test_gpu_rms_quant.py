@@ -107,3 +107,34 @@ def test_inputs_not_mutated_and_repeatable(device):
     a = rms_quantize(x, gamma, signs, 128)
     b = rms_quantize(x, gamma, signs, 128)
     assert torch.equal(x, before) and torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def _folded_codes_fp32(x32, gamma, signs, block):
+    """The folded quantizer's code chain in FP32, independent of its reduction order:
+    z = H(fl(x * gamma) * sign) in the pinned sequential stage order (c_hadamard_f32),
+    peak = max |z|, code = clamp(rint(fl(fl(z / peak) * 127)), -127, 127) (0 for a zero peak)."""
+    z = ref.c_hadamard_f32((x32 * gamma).astype(np.float32), block, signs)
+    peak = np.max(np.abs(z), axis=1, keepdims=True).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        v = ((z / np.where(peak == 0, np.float32(1), peak)).astype(np.float32) * np.float32(127)).astype(np.float32)
+    q = np.clip(np.rint(v), -127, 127).astype(np.int8)
+    return np.where(peak == 0, np.int8(0), q)
+
+
+@pytest.mark.parametrize("block", [128, 256])
+def test_folded_codes_bit_exact_fp32_chain(block, device):
+    """Codes of the folded quantizer equal the FP32 chain rint(fl(fl(z/peak)*127)) bit for bit
+    (they do not depend on the statistics' summation order), on ordinary rows, outlier rows, a
+    zero row and rows whose 127/peak leaves the encoder's fast range."""
+    rng = np.random.default_rng(block + 5)
+    x = rng.standard_normal((8, 4096)).astype(np.float32)
+    x[1, ::97] *= 80
+    x[2] = 0.0
+    x[3] *= np.float32(1e35)
+    x[4] *= np.float32(1e-33)
+    gamma = rng.uniform(0.5, 1.5, size=4096).astype(np.float32)
+    signs = ref.hadamard_signs(4096, 11)
+    xt = torch.from_numpy(x).to(device)
+    q, _ = rms_quantize(xt, torch.from_numpy(gamma).to(device), torch.from_numpy(signs).to(device), block,
+                        fold_scale=True)
+    np.testing.assert_array_equal(np_of(q), _folded_codes_fp32(x, gamma, signs, block))
