@@ -11,9 +11,11 @@
 // A row is read once from HBM with 16-byte loads and held in VGPRs between the max
 // reduction and the encode, so HBM traffic is exactly 2*K (bf16 in) + K (codes out) + 4
 // bytes per row.  Each row has its own workgroup of 4 wave64.  At [4096, 16384] the kernel
-// takes 37 us where the same traffic with no arithmetic streams in 26 us: the encode's ~7
-// VALU ops per element are the difference.  A persistent grid with a one-row register
-// prefetch, and a variant at 8 waves per SIMD, measured no faster.  Nor did four rows per
+// takes 36 us where the same traffic with no arithmetic streams in 26 us.  The difference is
+// the latency of each workgroup's row (all loads, the block reduction, then the encode), not
+// VALU throughput: the encode is ~8 VALU ops per element and the VALU is 34% busy.  A
+// persistent grid with a one-row register prefetch, and a variant at 8 waves per SIMD,
+// measured no faster.  Nor did four rows per
 // workgroup, unrolled so that each row's loads stay in flight across the previous row's
 // reduction (an LDS-only barrier, exact vmcnt waits): 40.6 us against 37.9 us for INT8, the
 // halved occupancy (118 VGPRs) costing more than the overlap gains.  Giving each thread two
