@@ -173,8 +173,16 @@ def time_op(torch, fn, reps=20, warm=10):
             "per_call_avg_ms": statistics.fmean(ts)}
 
 
-def _gemm_case(torch, dev, m, k, n, seed, mode="int8", outlier_every=None):
-    """Online W quantized offline; step = quantize(A) + GEMM -> BF16."""
+def _rel_l2(actual, reference):
+    import numpy as np
+
+    return float(np.linalg.norm(actual - reference) / np.linalg.norm(reference))
+
+
+def _gemm_case(torch, dev, m, k, n, seed, mode="int8", outlier_every=None, bf16_compare=False):
+    """Online W quantized offline; step = quantize(A) + GEMM -> BF16.  With bf16_compare, also
+    the BF16 torch F.linear of the same A and W (timed the same way) and both outputs' rel-L2
+    against the float64 product on 32 rows spread over M (the reference's sampled-row check)."""
     from m5kernels_amd import gemm, quantize
 
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -193,6 +201,19 @@ def _gemm_case(torch, dev, m, k, n, seed, mode="int8", outlier_every=None):
 
     step = time_op(torch, online)
     only = time_op(torch, lambda: gemm(aq, wq, mode, a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16))
+    compare = {}
+    if bf16_compare:
+        import numpy as np
+
+        bf = time_op(torch, lambda: torch.nn.functional.linear(a, w))
+        rows = torch.linspace(0, m - 1, 32).round().long().to(dev)
+        exact = a[rows].double().cpu().numpy() @ w.double().cpu().numpy().T
+        y8 = online()[rows].float().cpu().numpy().astype(np.float64)
+        y16 = torch.nn.functional.linear(a, w)[rows].float().cpu().numpy().astype(np.float64)
+        compare = {"bf16_linear_ms": bf["avg_ms"], "bf16_linear_TFLOPs": ops / (bf["avg_ms"] * 1e-3) / 1e12,
+                   "online_speedup_over_bf16": bf["avg_ms"] / step["avg_ms"],
+                   "rel_l2_vs_float64_w8a8": _rel_l2(y8, exact), "rel_l2_vs_float64_bf16": _rel_l2(y16, exact),
+                   "rel_l2_rows": "32 rows spread over M, full K, all N"}
     return {
         "shape": {"m": m, "k": k, "n": n},
         "mode": mode,
@@ -203,6 +224,7 @@ def _gemm_case(torch, dev, m, k, n, seed, mode="int8", outlier_every=None):
         "gemm_frac_of_peak": ops / (only["avg_ms"] * 1e-3) / 1e12 / PEAK_INT8_TOPS,
         "gemm_weight_GBps": n * k / (only["avg_ms"] * 1e-3) / 1e9,  # the bound that matters at short M
         "online_p10_p90_ms": [step["p10_ms"], step["p90_ms"]],
+        **compare,
     }
 
 
@@ -466,7 +488,7 @@ def extras(torch, dev):
     cases = [
         ("ffn_down_fp8_online", lambda: _gemm_case(torch, dev, M, K, N, SEED, "fp8", 1024)),
         ("ffn_down_h128_int8_online", lambda: _hadamard_case(torch, dev)),
-        ("q_proj_4096_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 4096, SEED)),
+        ("q_proj_4096_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 4096, SEED, bf16_compare=True)),
         ("ffn_up_int8_online", lambda: _gemm_case(torch, dev, 4096, 4096, 16384, SEED)),
         ("ffn_down_m128_int8_online_splitk", lambda: _gemm_case(torch, dev, 128, K, N, SEED)),
         ("q_proj_m128_int8_online_splitk", lambda: _gemm_case(torch, dev, 128, 4096, 4096, SEED)),
