@@ -65,53 +65,51 @@ __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) 
   const int tid = threadIdx.x;
   const int64_t nchunks = p.k / EPC;
   const float kf = static_cast<float>(p.k);
-  float v[NV];
+  // Every load of the row (x, gamma and signs of all chunks) is issued before any value is
+  // used, so their latencies overlap.  A lane whose chunk lies past the row end reads chunk 0
+  // (in bounds) and zeroes what it read.
+  float v[NV], g[NV];
+  uint2 sg[NV / 8];
   bool live[NCH];
-  float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int64_t c = tid + static_cast<int64_t>(i) * kThreads;
     live[i] = c < nchunks;
+    const int64_t j0 = (live[i] ? c : 0) * EPC;
 #pragma unroll
     for (int h = 0; h < EPC / 8; ++h) {
+      const int64_t j = j0 + 8 * h;
       float t[8];
-      if (live[i]) {
-        load8x<XDT>(p.x, row * p.k + c * EPC + 8 * h, t);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) t[r] = 0.0f;
-      }
+      load8x<XDT>(p.x, row * p.k + j, t);
+      const float4 g0 = *reinterpret_cast<const float4*>(p.gamma + j);
+      const float4 g1 = *reinterpret_cast<const float4*>(p.gamma + j + 4);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      sg[(i * EPC) / 8 + h] = *reinterpret_cast<const uint2*>(p.signs + j);
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        v[i * EPC + 8 * h + r] = t[r];
-        ss += t[r] * t[r];
+        v[i * EPC + 8 * h + r] = live[i] ? t[r] : 0.0f;
+        g[i * EPC + 8 * h + r] = live[i] ? gg[r] : 0.0f;
       }
     }
   }
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV; ++e) ss += v[e] * v[e];
   float inv = 1.0f;
   if constexpr (!FOLD) inv = 1.0f / sqrtf(block_sum<kWaves>(ss, red) / kf + p.eps);
   float peak = 0.0f;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    const int64_t c = tid + static_cast<int64_t>(i) * kThreads;
     float z[EPC];
 #pragma unroll
     for (int h = 0; h < EPC / 8; ++h) {
-      if (live[i]) {
-        const int64_t j = c * EPC + 8 * h;
-        const float4 g0 = *reinterpret_cast<const float4*>(p.gamma + j);
-        const float4 g1 = *reinterpret_cast<const float4*>(p.gamma + j + 4);
-        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const uint2 sg = *reinterpret_cast<const uint2*>(p.signs + j);
+      const uint2 sw = sg[(i * EPC) / 8 + h];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const float s = static_cast<float>(static_cast<int8_t>(((r < 4 ? sg.x : sg.y) >> (8 * (r & 3))) & 0xFFu));
-          const float x = v[i * EPC + 8 * h + r];
-          z[8 * h + r] = FOLD ? (x * g[r]) * s : ((x * inv) * g[r]) * s;
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) z[8 * h + r] = 0.0f;
+      for (int r = 0; r < 8; ++r) {
+        const float s = static_cast<float>(static_cast<int8_t>(((r < 4 ? sw.x : sw.y) >> (8 * (r & 3))) & 0xFFu));
+        const float x = v[i * EPC + 8 * h + r];
+        const float gr = g[i * EPC + 8 * h + r];
+        z[8 * h + r] = FOLD ? (x * gr) * s : ((x * inv) * gr) * s;
       }
     }
     hadamard::butterflies<B, false>(z);
