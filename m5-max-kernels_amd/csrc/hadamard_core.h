@@ -8,7 +8,11 @@
 // Register layout: a lane holds EPC = max(8, B/64) consecutive elements of a block, so
 // one block spans LPB = B/EPC <= 64 consecutive lanes.  Strides below EPC stay inside
 // a lane's registers; strides EPC..B/2 are lane-xor exchanges within the LPB-lane group
-// (the upper lane of a pair computes lower - upper, as an FMA with -1).  Each stage output
+// (the upper lane of a pair computes lower - upper, as an FMA with -1).  Partners within 32
+// lanes come through ds_swizzle in its bit-mask mode, the partner 32 lanes away through
+// v_permlane32_swap (one pass leaves the lower half's value in one register and the upper
+// half's in the other on every lane).  With ds_bpermute, which reads an address per lane, the
+// B = 256 RMS-quantize row kernel took 1.5x as long.  Each stage output
 // is one correctly rounded FP32 sum or difference of its two inputs, so the result is
 // independent of which lane does the work and bit-identical to a sequential FP32
 // evaluation of the same stages.
@@ -37,6 +41,30 @@ __device__ __forceinline__ constexpr float inv_sqrt_block() {
                     : 0x1.0p-5f;
 }
 
+// Lane-xor stages M, 2M, ..., LPB/2 of the transform.  fma(+-1, v, peer) is the single
+// rounding of v + peer (lower lane) or peer - v (upper lane): the same bits as the add or
+// subtract, in one VALU op instead of add, sub, select.
+template <int M, int LPB, int EPC>
+__device__ __forceinline__ void cross_stages(float (&v)[EPC], int lane) {
+  if constexpr (M < LPB) {
+    const float sgn = (lane & M) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int r = 0; r < EPC; ++r) {
+      if constexpr (M < 32) {
+        // Bit-mask swizzle within 32 lanes: and 0x1F, or 0, xor M.
+        const float peer = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[r]), 0x1F | (M << 10)));
+        v[r] = __builtin_fmaf(sgn, v[r], peer);
+      } else {
+        // Both operands v: afterwards the first holds lanes 0-31's value and the second lanes
+        // 32-63's, on every lane; lower + upper or lower - upper is fma(sgn, upper, lower).
+        const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[r]), __float_as_uint(v[r]), false, false);
+        v[r] = __builtin_fmaf(sgn, __uint_as_float(halves[1]), __uint_as_float(halves[0]));
+      }
+    }
+    cross_stages<2 * M, LPB>(v, lane);
+  }
+}
+
 // In-place transform of v[EPC] for the calling lane (all lanes of a block must call).
 // SCALED = false leaves out the final multiply by 1/sqrt(B); FoldedI8 applies it inside the
 // quantizer's encode instead.
@@ -55,15 +83,7 @@ __device__ __forceinline__ void butterflies(float (&v)[Shape<B>::EPC]) {
       }
     }
   }
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int m = 1; m < LPB; m <<= 1) {
-    // fma(+-1, v, peer) is the single rounding of v + peer (lower lane) or peer - v (upper
-    // lane): the same bits as the add or subtract, in one VALU op instead of add, sub, select.
-    const float sgn = (lane & m) ? -1.0f : 1.0f;
-#pragma unroll
-    for (int r = 0; r < EPC; ++r) v[r] = __builtin_fmaf(sgn, v[r], __shfl_xor(v[r], m, 64));
-  }
+  cross_stages<1, LPB>(v, static_cast<int>(threadIdx.x & 63));
   if constexpr (SCALED) {
     constexpr float inv = inv_sqrt_block<B>();
 #pragma unroll

@@ -67,7 +67,9 @@ __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) 
   const float kf = static_cast<float>(p.k);
   // Every load of the row (x, gamma and signs of all chunks) is issued before any value is
   // used, so their latencies overlap.  A lane whose chunk lies past the row end reads chunk 0
-  // (in bounds) and zeroes what it read.
+  // (in bounds) and zeroes what it read; rows with no such chunk (nchunks a multiple of the
+  // workgroup width, uniform) skip the selects.
+  const bool ragged = nchunks < static_cast<int64_t>(NCH) * kThreads;
   float v[NV], g[NV];
   uint2 sg[NV / 8];
   bool live[NCH];
@@ -87,14 +89,26 @@ __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) 
       sg[(i * EPC) / 8 + h] = *reinterpret_cast<const uint2*>(p.signs + j);
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        v[i * EPC + 8 * h + r] = live[i] ? t[r] : 0.0f;
-        g[i * EPC + 8 * h + r] = live[i] ? gg[r] : 0.0f;
+        v[i * EPC + 8 * h + r] = t[r];
+        g[i * EPC + 8 * h + r] = gg[r];
       }
     }
   }
+  if (ragged) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+#pragma unroll
+      for (int r = 0; r < EPC; ++r) {
+        v[i * EPC + r] = live[i] ? v[i * EPC + r] : 0.0f;
+        g[i * EPC + r] = live[i] ? g[i * EPC + r] : 0.0f;
+      }
+    }
+  }
+  // The statistics feed only the inverse RMS; the sum of squares takes one fma per element
+  // (its order is this kernel's own either way).
   float ss = 0.0f;
 #pragma unroll
-  for (int e = 0; e < NV; ++e) ss += v[e] * v[e];
+  for (int e = 0; e < NV; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
   float inv = 1.0f;
   if constexpr (!FOLD) inv = 1.0f / sqrtf(block_sum<kWaves>(ss, red) / kf + p.eps);
   float peak = 0.0f;
@@ -114,9 +128,10 @@ __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) 
     }
     hadamard::butterflies<B, false>(z);
 #pragma unroll
-    for (int r = 0; r < EPC; ++r) {
+    for (int r = 0; r < EPC; r += 2) {
       v[i * EPC + r] = z[r];
-      peak = fmaxf(peak, fabsf(z[r]));
+      v[i * EPC + r + 1] = z[r + 1];
+      peak = fmaxf(peak, fmaxf(fabsf(z[r]), fabsf(z[r + 1])));
     }
   }
   // The butterflies leave out the 1/sqrt(B) multiply: the reference's z is fl(z' * c), whose
