@@ -55,10 +55,28 @@ __device__ __forceinline__ uint32_t rms_code(float z, float peak) {
   return peak == 0.0f ? 0u : i8_clamp_code(rintf((z / peak) * 127.0f));
 }
 
+// Workgroup max of m and sum of s through one barrier: the same wave reductions and the same
+// in-order combination of the wave partials as block_max and block_sum.
+__device__ __forceinline__ float2 block_max_sum(float m, float s, float2* lds) {
+  m = wave_max(m);
+  s = wave_sum(s);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = make_float2(m, s);
+  __syncthreads();
+  float2 r = lds[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    r.x = fmaxf(r.x, lds[w].x);
+    r.y += lds[w].y;
+  }
+  return r;
+}
+
 // Block-Hadamard variant (B >= 32, K % B == 0).
 template <int XDT, int B, int NCH, bool FOLD>
 __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) {
-  __shared__ float red[3 * kWaves];  // one slot per block reduction
+  __shared__ float red[2 * kWaves];  // unfolded: statistics, then peak
+  __shared__ float2 red2[kWaves];    // folded: peak and sum of squares
   constexpr int EPC = Shape<B>::EPC;
   constexpr int NV = NCH * EPC;
   const int64_t row = blockIdx.x;
@@ -140,9 +158,16 @@ __global__ __launch_bounds__(kThreads) void rms_quant_block_kernel(RmsParams p) 
   // by the estimate m~ = fl(c * fl(127 / peak)) (two roundings; 0 for a zero or infinite peak,
   // where every finite z codes to 0).
   constexpr float c = hadamard::inv_sqrt_block<B>();
-  peak = block_max<kWaves>(peak, red + kWaves) * c;
-  if constexpr (FOLD) inv = 1.0f / sqrtf(block_sum<kWaves>(ss, red + 2 * kWaves) / kf + p.eps);
-  if (tid == 0) p.scales[row] = peak == 0.0f ? 1.0f : (FOLD ? peak * inv : peak) / 127.0f;
+  if constexpr (FOLD) {
+    // Peak and sum of squares share one barrier; only the lane that writes the scale needs
+    // the inverse RMS.
+    const float2 ps = block_max_sum(peak, ss, red2);
+    peak = ps.x * c;
+    if (tid == 0) p.scales[row] = peak == 0.0f ? 1.0f : (peak * (1.0f / sqrtf(ps.y / kf + p.eps))) / 127.0f;
+  } else {
+    peak = block_max<kWaves>(peak, red + kWaves) * c;
+    if (tid == 0) p.scales[row] = peak == 0.0f ? 1.0f : peak / 127.0f;
+  }
   const I8Bracket enc = i8_bracket(peak == 0.0f ? 0.0f : c * (127.0f / peak), false);
   const auto chain = [peak](float zu) { return rms_code(zu * c, peak); };
 #pragma unroll
