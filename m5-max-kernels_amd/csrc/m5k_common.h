@@ -252,8 +252,11 @@ __device__ __forceinline__ void encode_i8_div(const float (&x)[N], const I8Scale
 // v_cvt_pk_fp8_f32 equals fp8_e4m3_encode on every finite f32 of magnitude below 464 (all
 // 2.28e9 of them compared on MI355X; |x * hi| <= 448.001 here) and is monotone in the value, so
 // when both products give the same code, fl(x / scale) gives it too.  Otherwise (or for an
-// out-of-range reciprocal) the call's values take the IEEE division and the software encoder,
-// on every lane of the wave.  A NaN input has no defined code.
+// out-of-range reciprocal) the call's values take the IEEE division, on every lane of the wave,
+// and the same conversion of the quotient; quotients at or above 448 in magnitude saturate first
+// as fp8_e4m3_encode does.  Exact ties of fl(x / scale) are common for 16-bit inputs (an E4M3
+// midpoint has 4 significant bits), so this path runs for a sizeable share of groups; the
+// conversion keeps it at the division's cost.
 template <int N>
 __device__ __forceinline__ void encode_fp8(const float (&x)[N], const I8Scale& s, uint32_t (&out)[N / 4]) {
   const I8Bracket e = i8_bracket(s.inv, s.exact);
@@ -269,12 +272,20 @@ __device__ __forceinline__ void encode_fp8(const float (&x)[N], const I8Scale& s
     out[w] = static_cast<uint32_t>(hi);
   }
   if (unsettled) {
+    // The exact chain: the IEEE quotient through the same conversion.  A quotient of magnitude
+    // 448 or more, infinite or NaN enters as 448 with its sign bit, which converts to the
+    // software encoder's saturated code (126 and the sign bit).
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
-      uint32_t word = 0;
+      float q[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) word |= fp8_e4m3_encode(x[4 * w + b] / s.scale) << (8 * b);
-      out[w] = word;
+      for (int b = 0; b < 4; ++b) {
+        const float z = x[4 * w + b] / s.scale;
+        q[b] = fabsf(z) < 448.0f ? z : copysignf(448.0f, z);
+      }
+      int c = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+      c = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], c, true);
+      out[w] = static_cast<uint32_t>(c);
     }
   }
 }
