@@ -38,38 +38,63 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(const void* __restrict
   }
 }
 
+// One row per workgroup.  Every load of the row (x and signs of all CPT chunks) is issued
+// before the first wait; a chunk past the row end (only when nchunks is not a multiple of the
+// workgroup width, a uniform test) reads chunk 0, which is in bounds, and is zeroed.  The signs
+// (+-1) enter as sign-bit flips of the packed words, the exact product with +-1.
 template <int DT, int B, int CPT>
 __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(const void* __restrict__ x, int64_t k,
                                                                 const int8_t* __restrict__ signs,
                                                                 int8_t* __restrict__ q, float* __restrict__ scales) {
   __shared__ float red[kThreads / 64];
   constexpr int EPC = Shape<B>::EPC;
+  constexpr int G = EPC / 8;  // 8-element groups per chunk
   const int64_t row = blockIdx.x;
   const int64_t nchunks = k / EPC;
+  const bool ragged = nchunks < static_cast<int64_t>(CPT) * kThreads;
+  const uint8_t* xrow = static_cast<const uint8_t*>(x) + row * k * dtype_bytes<DT>();
+  Raw8<DT> xr[CPT][G];
+  uint2 sr[CPT][G];
+  bool live[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+    live[i] = c < nchunks;
+    const uint32_t j0 = static_cast<uint32_t>((live[i] ? c : 0) * EPC);
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      xr[i][t] = fetch8_at<DT>(xrow, j0 + 8 * t);
+      sr[i][t] = *reinterpret_cast<const uint2*>(signs + j0 + 8 * t);
+    }
+  }
   float v[CPT][EPC];
   float peak = 0.0f;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
-    if (c < nchunks) {
-      load_signed<DT, EPC>(x, row * k + c * EPC, signs, c * EPC, v[i]);
-    } else {
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      float f[8];
+      decode8<DT>(SignMask8<DT>(sr[i][t]).apply(xr[i][t]), f);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) v[i][8 * t + b] = f[b];
+    }
+    if (ragged && !live[i]) {
 #pragma unroll
       for (int r = 0; r < EPC; ++r) v[i][r] = 0.0f;
     }
     butterflies<B, false>(v[i]);
 #pragma unroll
-    for (int r = 0; r < EPC; ++r) peak = fmaxf(peak, fabsf(v[i][r]));
+    for (int r = 0; r < EPC; r += 2) peak = fmaxf(peak, fmaxf(fabsf(v[i][r]), fabsf(v[i][r + 1])));
   }
   const FoldedI8<B> enc(block_max<kThreads / 64>(peak, red));
   if (threadIdx.x == 0) scales[row] = enc.scale;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
-    if (c < nchunks) {
+    if (live[i]) {
+      const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
       uint2* out = reinterpret_cast<uint2*>(q + row * k + c * EPC);
 #pragma unroll
-      for (int t = 0; t < EPC / 8; ++t) {
+      for (int t = 0; t < G; ++t) {
         float g[8];
 #pragma unroll
         for (int b = 0; b < 8; ++b) g[b] = v[i][8 * t + b];

@@ -112,6 +112,81 @@ struct FoldedI8 {
   }
 };
 
+// Raw 16-byte words of 8 elements of dtype DT (one word for 2-byte types, two for FP32).
+template <int DT>
+struct Raw8 {
+  uint4 w[dtype_bytes<DT>() / 2];
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> fetch8(const void* base, int64_t e) {
+  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) + e * dtype_bytes<DT>());
+  Raw8<DT> r;
+#pragma unroll
+  for (int i = 0; i < dtype_bytes<DT>() / 2; ++i) r.w[i] = p[i];
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void decode8(const Raw8<DT>& r, float (&v)[8]) {
+  if constexpr (DT == M5K_F32) {
+    const uint32_t w[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+  } else {
+    const uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == M5K_BF16) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      } else {
+        v[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
+// 8 elements at column `col` of a row whose base address is uniform (a 32-bit lane offset).
+template <int DT>
+__device__ __forceinline__ Raw8<DT> fetch8_at(const uint8_t* row_base, uint32_t col) {
+  const uint4* q = reinterpret_cast<const uint4*>(row_base + col * static_cast<uint32_t>(dtype_bytes<DT>()));
+  Raw8<DT> r;
+#pragma unroll
+  for (int i = 0; i < dtype_bytes<DT>() / 2; ++i) r.w[i] = q[i];
+  return r;
+}
+
+// Sign-bit masks of 8 columns for their 16-byte words of dtype DT (BF16/FP16 words hold elements
+// 2i and 2i + 1 in bits 0-15 and 16-31; FP32 words one element each): XOR flips the sign of each
+// column whose int8 sign is negative, the exact product with +-1.  v_perm_b32 moves sign bytes 2i and 2i + 1 to bytes 1 and 3 (selector
+// 0x0C yields zero), the AND keeps their top bits.
+template <int PDT>
+struct SignMask8 {
+  uint32_t m[PDT == M5K_F32 ? 8 : 4];
+  __device__ __forceinline__ explicit SignMask8(const uint2& s) {
+    if constexpr (PDT == M5K_F32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m[i] = ((i < 4 ? s.x : s.y) << (24 - 8 * (i & 3))) & 0x80000000u;
+    } else {
+      m[0] = __builtin_amdgcn_perm(0u, s.x, 0x010C000Cu) & 0x80008000u;
+      m[1] = __builtin_amdgcn_perm(0u, s.x, 0x030C020Cu) & 0x80008000u;
+      m[2] = __builtin_amdgcn_perm(0u, s.y, 0x010C000Cu) & 0x80008000u;
+      m[3] = __builtin_amdgcn_perm(0u, s.y, 0x030C020Cu) & 0x80008000u;
+    }
+  }
+  __device__ __forceinline__ Raw8<PDT> apply(Raw8<PDT> r) const {
+    if constexpr (PDT == M5K_F32) {
+      r.w[0].x ^= m[0]; r.w[0].y ^= m[1]; r.w[0].z ^= m[2]; r.w[0].w ^= m[3];
+      r.w[1].x ^= m[4]; r.w[1].y ^= m[5]; r.w[1].z ^= m[6]; r.w[1].w ^= m[7];
+    } else {
+      r.w[0].x ^= m[0]; r.w[0].y ^= m[1]; r.w[0].z ^= m[2]; r.w[0].w ^= m[3];
+    }
+    return r;
+  }
+};
+
 // Load EPC consecutive elements of dtype DT starting at element index e (16-byte aligned
 // when the caller checked alignment) and apply the shared signs.
 template <int DT, int EPC>
