@@ -106,6 +106,7 @@ struct LaneRope {
   float gam[8];  // gamma of the lane's channels
   int src;       // partner lane within the 16-lane group
   bool rot, lower;
+  float sgn;     // -1 for the lower half of the rotated channels, else +1
 };
 
 __device__ __forceinline__ LaneRope lane_rope(const QkParams& p, const uint16_t* gamma, int lg) {
@@ -121,6 +122,7 @@ __device__ __forceinline__ LaneRope lane_rope(const QkParams& p, const uint16_t*
   r.rot = d0 < 2 * R;
   r.lower = d0 < R;
   r.src = !r.rot ? lg : r.lower ? lg + R / 8 : lg - R / 8;
+  r.sgn = r.lower ? -1.0f : 1.0f;
   return r;
 }
 
@@ -160,34 +162,70 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// Normalize + rotate one (row, head) held as z[8] per lane; returns the packed BF16 output.
-// HALF8: rope_half == 64, every partner lane is lg ^ 8 (one row_ror:8 DPP move).
-template <bool HALF8>
-__device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneRope& r, const uint4& cw,
-                                                const uint4& sw, float eps) {
+// Sum of squares of one (row, head) held as z[8] per lane of its 16-lane group, in every lane.
+__device__ __forceinline__ float head_sumsq(const float (&z)[8]) {
   float ss = 0.0f;
 #pragma unroll
   for (int t = 0; t < 8; ++t) ss += z[t] * z[t];
-  ss = row16_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(HEAD) + eps);
+  return row16_sum(ss);
+}
+
+__device__ __forceinline__ float head_inv(float ss, float eps) {
+  return 1.0f / sqrtf(ss / static_cast<float>(HEAD) + eps);
+}
+
+// Lane k's value of each 16-lane row (row_newbcast:k), for k known after unrolling.
+__device__ __forceinline__ float row16_bcast(float v, int k) {
+  switch (k) {
+    case 0: return dpp_move<0x150>(v);
+    case 1: return dpp_move<0x151>(v);
+    case 2: return dpp_move<0x152>(v);
+    case 3: return dpp_move<0x153>(v);
+    case 4: return dpp_move<0x154>(v);
+    case 5: return dpp_move<0x155>(v);
+    case 6: return dpp_move<0x156>(v);
+    case 7: return dpp_move<0x157>(v);
+    case 8: return dpp_move<0x158>(v);
+    case 9: return dpp_move<0x159>(v);
+    case 10: return dpp_move<0x15A>(v);
+    case 11: return dpp_move<0x15B>(v);
+    case 12: return dpp_move<0x15C>(v);
+    case 13: return dpp_move<0x15D>(v);
+    case 14: return dpp_move<0x15E>(v);
+    default: return dpp_move<0x15F>(v);
+  }
+}
+
+// Normalize (by the head's inverse RMS `inv`) and rotate one (row, head) held as z[8] per
+// lane; returns the packed BF16 output.  HALF8: rope_half == 64, every partner lane is lg ^ 8
+// (one row_ror:8 DPP move).
+template <bool HALF8>
+__device__ __forceinline__ uint4 rope_apply(const float (&z)[8], const LaneRope& r, const uint4& cw,
+                                            const uint4& sw, float inv) {
   float u[8], c[8], s[8];
   unpack8_bf16(cw, c);
   unpack8_bf16(sw, s);
 #pragma unroll
   for (int t = 0; t < 8; ++t) u[t] = (z[t] * inv) * r.gam[t];
-  uint32_t packed[4];
+  // All partner values first, then branch-free arithmetic: fma(-+1, b, a) is the single
+  // rounding of a - b (lower half) or a + b (upper half), the same bits as the subtract or add.
+  float pu[8];
 #pragma unroll
-  for (int t = 0; t < 8; t += 2) {
-    float y[2];
+  for (int t = 0; t < 8; ++t) pu[t] = HALF8 ? dpp_move<0x128>(u[t]) : __shfl(u[t], r.src, 16);
+  float y[8];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const float pu = HALF8 ? dpp_move<0x128>(u[t + e]) : __shfl(u[t + e], r.src, 16);
-      const float a = u[t + e] * c[t + e], b = pu * s[t + e];
-      y[e] = !r.rot ? u[t + e] : r.lower ? a - b : a + b;
-    }
-    packed[t / 2] = f32x2_to_bf16x2(y[0], y[1]);
+  for (int t = 0; t < 8; ++t) {
+    const float rotated = __builtin_fmaf(r.sgn, pu[t] * s[t], u[t] * c[t]);
+    y[t] = r.rot ? rotated : u[t];
   }
-  return make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  return make_uint4(f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3]), f32x2_to_bf16x2(y[4], y[5]),
+                    f32x2_to_bf16x2(y[6], y[7]));
+}
+
+template <bool HALF8>
+__device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneRope& r, const uint4& cw,
+                                                const uint4& sw, float eps) {
+  return rope_apply<HALF8>(z, r, cw, sw, head_inv(head_sumsq(z), eps));
 }
 
 // Epilogue of one 256 x G::TN projection tile (G::TN = 256: two heads, or 128: one head), called
@@ -261,27 +299,47 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
   __syncthreads();
 
   if (fast) {
+    // The group's (row, head) pairs, pair k = HPT i + h, at most one per lane.  A first pass
+    // forms every pair's sum of squares and lane k keeps pair k's, so each lane takes one
+    // square root and division; the second broadcasts pair k's inverse from lane k.  Pairs of
+    // rows past M are read from the staged tile (inside it) and store nothing.
+    constexpr int PAIRS = ROWS_PER_GROUP * HPT;
+    static_assert(PAIRS <= 16, "one (row, head) pair per lane of the group");
+    uint4 w[PAIRS];
+    float ss_mine = 0.0f;
 #pragma unroll
     for (int i = 0; i < ROWS_PER_GROUP; ++i) {
-      const int local_row = group + GROUPS * i;
-      const int row = m0 + local_row;
+#pragma unroll
+      for (int h = 0; h < HPT; ++h) {
+        const int k = HPT * i + h;
+        w[k] = *reinterpret_cast<const uint4*>(tile + (group + GROUPS * i) * TILE16_STRIDE + h * HEAD + 8 * lg);
+        float z[8];
+        unpack8_bf16(w[k], z);
+        const float ss = head_sumsq(z);
+        ss_mine = lg == k ? ss : ss_mine;
+      }
+    }
+    const float inv_mine = head_inv(ss_mine, p.eps);
+#pragma unroll
+    for (int i = 0; i < ROWS_PER_GROUP; ++i) {
+      const int row = m0 + group + GROUPS * i;
       if (row >= M) continue;  // uniform across the 16-lane group
 #pragma unroll
       for (int h = 0; h < HPT; ++h) {
         if (h >= heads_here) continue;
-        const uint16_t* src = tile + local_row * TILE16_STRIDE + h * HEAD;
+        const int k = HPT * i + h;
         const BlockDst d = block_dst(p, n0 / HEAD + h);  // uniform across the group
-        const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lg);
         uint4* dst = reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg);
         if (d.gamma == nullptr) {  // V: the rounded projection
-          *dst = w;
+          *dst = w[k];
           continue;
         }
         float z[8];
-        unpack8_bf16(w, z);
+        unpack8_bf16(w[k], z);
         const LaneRope& rr = d.gamma == p.gamma ? lr : lrk;
-        *dst = p.rope_half == 64 ? norm_rope_fast<true>(z, rr, cw[i], sw[i], p.eps)
-                                 : norm_rope_fast<false>(z, rr, cw[i], sw[i], p.eps);
+        const float inv = row16_bcast(inv_mine, k);
+        *dst = p.rope_half == 64 ? rope_apply<true>(z, rr, cw[i], sw[i], inv)
+                                 : rope_apply<false>(z, rr, cw[i], sw[i], inv);
       }
     }
     return;
