@@ -10,12 +10,12 @@
 //
 // A row is read once from HBM with 16-byte loads and held in VGPRs between the max
 // reduction and the encode, so HBM traffic is exactly 2*K (bf16 in) + K (codes out) + 4
-// bytes per row.  Each row has its own workgroup of 4 wave64.  At [4096, 16384] the kernel
-// takes 36 us where the same traffic with no arithmetic streams in 26 us.  The difference is
-// the latency of each workgroup's row (all loads, the block reduction, then the encode), not
-// VALU throughput: the encode is ~8 VALU ops per element and the VALU is 34% busy.  A
-// persistent grid with a one-row register prefetch, and a variant at 8 waves per SIMD,
-// measured no faster.  Nor did four rows per
+// bytes per row.  Each row has its own workgroup of 256, 512 or 1024 threads, as many as
+// give each thread about two 16-byte chunks (see launch_quantize).  At [4096, 16384] the
+// kernel takes ~30 us where the same traffic with no arithmetic streams in 26 us: a row's
+// time is its loads, one block reduction, then its encode, and a wider workgroup shortens
+// the last two.  A persistent grid with a one-row register prefetch, and a variant at 8
+// waves per SIMD, measured no faster with 256 threads per row.  Nor did four rows per
 // workgroup, unrolled so that each row's loads stay in flight across the previous row's
 // reduction (an LDS-only barrier, exact vmcnt waits): 40.6 us against 37.9 us for INT8, the
 // halved occupancy (118 VGPRs) costing more than the overlap gains.  Giving each thread two
@@ -99,44 +99,44 @@ __device__ __forceinline__ void encode_chunk(const uint4& v, const I8Scale& s, u
   else *reinterpret_cast<uint32_t*>(out) = packed[0];
 }
 
-// Load a row's chunks tid, tid + 256, ... into registers; chunks past the row read as zero.
-template <int CPT>
+// Load a row's chunks tid, tid + KT, ... into registers; chunks past the row read as zero.
+template <int CPT, int KT>
 __device__ __forceinline__ void load_row(const uint4* __restrict__ xr, int64_t nchunks, int tid, uint4 (&v)[CPT]) {
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = tid + (int64_t)i * kThreads;
+    const int64_t c = tid + (int64_t)i * KT;
     v[i] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
   }
 }
 
-template <int DT, int MODE, int CPT>
+template <int DT, int MODE, int CPT, int KT>
 __device__ __forceinline__ void store_row(const uint4 (&v)[CPT], const I8Scale& s, int64_t nchunks, int tid,
                                           uint8_t* __restrict__ qr) {
   constexpr int EPC = 16 / dtype_bytes<DT>();
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = tid + (int64_t)i * kThreads;
+    const int64_t c = tid + (int64_t)i * KT;
     if (c < nchunks) encode_chunk<DT, MODE>(v[i], s, qr + c * EPC);
   }
 }
 
-// One workgroup per row: row bytes % 16 == 0 and 16-byte aligned bases.  CPT = 16-byte
-// chunks per thread kept in registers.
-template <int DT, int MODE, int CPT>
-__global__ __launch_bounds__(kThreads) void quantize_rows_vec(const uint8_t* __restrict__ x, int64_t k,
-                                                                uint8_t* __restrict__ q,
-                                                                float* __restrict__ scales) {
-  __shared__ float red[kWaves];
+// One workgroup of KT threads per row: row bytes % 16 == 0 and 16-byte aligned bases.  CPT =
+// 16-byte chunks per thread kept in registers.
+template <int DT, int MODE, int CPT, int KT>
+__global__ __launch_bounds__(KT) void quantize_rows_vec(const uint8_t* __restrict__ x, int64_t k,
+                                                          uint8_t* __restrict__ q,
+                                                          float* __restrict__ scales) {
+  __shared__ float red[KT / 64];
   constexpr int EPC = 16 / dtype_bytes<DT>();
   const int64_t row = blockIdx.x;
   const int64_t nchunks = k / EPC;
   const int tid = threadIdx.x;
   uint4 v[CPT];
-  load_row<CPT>(reinterpret_cast<const uint4*>(x + row * k * dtype_bytes<DT>()), nchunks, tid, v);
-  const float peak = block_max<kWaves>(thread_absmax<DT, CPT>(v), red);
+  load_row<CPT, KT>(reinterpret_cast<const uint4*>(x + row * k * dtype_bytes<DT>()), nchunks, tid, v);
+  const float peak = block_max<KT / 64>(thread_absmax<DT, CPT>(v), red);
   const I8Scale s = i8_scale(quant_scale<MODE>(peak));
   if (tid == 0) scales[row] = s.scale;
-  store_row<DT, MODE, CPT>(v, s, nchunks, tid, q + row * k);
+  store_row<DT, MODE, CPT, KT>(v, s, nchunks, tid, q + row * k);
 }
 
 // Rows wider than 16 chunks per thread: two passes, the second re-reading the row.
@@ -247,9 +247,9 @@ __global__ __launch_bounds__(kThreads) void mx_to_bf16_kernel(const int8_t* __re
   *reinterpret_cast<uint4*>(y + t * 8) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-template <int DT, int MODE, int CPT>
+template <int DT, int MODE, int KT, int CPT>
 void launch_vec(const uint8_t* x, int64_t rows, int64_t k, uint8_t* q, float* s, hipStream_t st) {
-  quantize_rows_vec<DT, MODE, CPT><<<dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st>>>(x, k, q, s);
+  quantize_rows_vec<DT, MODE, CPT, KT><<<dim3(static_cast<unsigned>(rows)), dim3(KT), 0, st>>>(x, k, q, s);
 }
 
 template <int DT, int MODE>
@@ -260,12 +260,19 @@ int launch_quantize(const void* x, int64_t rows, int64_t k, void* q, float* s, h
   auto* qb = static_cast<uint8_t*>(q);
   const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
   const int64_t chunks = row_bytes / 16;
+  // Workgroup width: rows of more than 512 chunks take 512 or 1024 threads with two (or more)
+  // chunks each.  A wider workgroup finishes its row sooner, and at FFN-down ([4096, 16384]
+  // BF16, 2048 chunks) 1024 threads x 2 chunks measured 29.4 us against 30.2 us for 512 x 4
+  // and 32.0-32.7 us for 256 x 8; at K 4096 (512 chunks) 256 x 2 measured 9.3 us against 15.7
+  // us for 512 x 1.  The row peak is order-independent, so codes and scales do not depend on
+  // the width.
   if (!vec) quantize_rows_scalar<DT, MODE><<<grid, block, 0, st>>>(x, k, qb, s);
-  else if (chunks <= kThreads * 1) launch_vec<DT, MODE, 1>(xb, rows, k, qb, s, st);
-  else if (chunks <= kThreads * 2) launch_vec<DT, MODE, 2>(xb, rows, k, qb, s, st);
-  else if (chunks <= kThreads * 4) launch_vec<DT, MODE, 4>(xb, rows, k, qb, s, st);
-  else if (chunks <= kThreads * 8) launch_vec<DT, MODE, 8>(xb, rows, k, qb, s, st);
-  else if (chunks <= kThreads * 16) launch_vec<DT, MODE, 16>(xb, rows, k, qb, s, st);
+  else if (chunks <= 256) launch_vec<DT, MODE, 256, 1>(xb, rows, k, qb, s, st);
+  else if (chunks <= 512) launch_vec<DT, MODE, 256, 2>(xb, rows, k, qb, s, st);
+  else if (chunks <= 1024) launch_vec<DT, MODE, 512, 2>(xb, rows, k, qb, s, st);
+  else if (chunks <= 2048) launch_vec<DT, MODE, 1024, 2>(xb, rows, k, qb, s, st);
+  else if (chunks <= 4096) launch_vec<DT, MODE, 1024, 4>(xb, rows, k, qb, s, st);
+  else if (chunks <= 8192) launch_vec<DT, MODE, 1024, 8>(xb, rows, k, qb, s, st);
   else quantize_rows_wide<DT, MODE><<<grid, block, 0, st>>>(xb, k, qb, s);
   return launch_status("m5k_quantize_rows");
 }
