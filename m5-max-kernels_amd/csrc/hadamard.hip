@@ -42,23 +42,23 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(const void* __restrict
 // before the first wait; a chunk past the row end (only when nchunks is not a multiple of the
 // workgroup width, a uniform test) reads chunk 0, which is in bounds, and is zeroed.  The signs
 // (+-1) enter as sign-bit flips of the packed words, the exact product with +-1.
-template <int DT, int B, int CPT>
-__global__ __launch_bounds__(kThreads) void rotate_quant_kernel(const void* __restrict__ x, int64_t k,
-                                                                const int8_t* __restrict__ signs,
-                                                                int8_t* __restrict__ q, float* __restrict__ scales) {
-  __shared__ float red[kThreads / 64];
+template <int DT, int B, int CPT, int KT>
+__global__ __launch_bounds__(KT) void rotate_quant_kernel(const void* __restrict__ x, int64_t k,
+                                                          const int8_t* __restrict__ signs,
+                                                          int8_t* __restrict__ q, float* __restrict__ scales) {
+  __shared__ float red[KT / 64];
   constexpr int EPC = Shape<B>::EPC;
   constexpr int G = EPC / 8;  // 8-element groups per chunk
   const int64_t row = blockIdx.x;
   const int64_t nchunks = k / EPC;
-  const bool ragged = nchunks < static_cast<int64_t>(CPT) * kThreads;
+  const bool ragged = nchunks < static_cast<int64_t>(CPT) * KT;
   const uint8_t* xrow = static_cast<const uint8_t*>(x) + row * k * dtype_bytes<DT>();
   Raw8<DT> xr[CPT][G];
   uint2 sr[CPT][G];
   bool live[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+    const int64_t c = threadIdx.x + static_cast<int64_t>(i) * KT;
     live[i] = c < nchunks;
     const uint32_t j0 = static_cast<uint32_t>((live[i] ? c : 0) * EPC);
 #pragma unroll
@@ -86,12 +86,12 @@ __global__ __launch_bounds__(kThreads) void rotate_quant_kernel(const void* __re
 #pragma unroll
     for (int r = 0; r < EPC; r += 2) peak = fmaxf(peak, fmaxf(fabsf(v[i][r]), fabsf(v[i][r + 1])));
   }
-  const FoldedI8<B> enc(block_max<kThreads / 64>(peak, red));
+  const FoldedI8<B> enc(block_max<KT / 64>(peak, red));
   if (threadIdx.x == 0) scales[row] = enc.scale;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     if (live[i]) {
-      const int64_t c = threadIdx.x + static_cast<int64_t>(i) * kThreads;
+      const int64_t c = threadIdx.x + static_cast<int64_t>(i) * KT;
       uint2* out = reinterpret_cast<uint2*>(q + row * k + c * EPC);
 #pragma unroll
       for (int t = 0; t < G; ++t) {
@@ -115,19 +115,29 @@ int launch_rotate(const void* x, int64_t rows, int64_t k, const int8_t* signs, f
   return launch_status("m5k_hadamard_rotate");
 }
 
+template <int DT, int B, int CPT, int KT>
+void rq_launch(dim3 grid, const void* x, int64_t k, const int8_t* signs, int8_t* q, float* s, hipStream_t st) {
+  rotate_quant_kernel<DT, B, CPT, KT><<<grid, dim3(KT), 0, st>>>(x, k, signs, q, s);
+}
+
 template <int DT, int B>
 int launch_rotate_quant(const void* x, int64_t rows, int64_t k, const int8_t* signs, int8_t* q, float* s,
                         hipStream_t st) {
-  const int64_t per_thread = (k / Shape<B>::EPC + kThreads - 1) / kThreads;
-  const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
-  if (per_thread <= 1) rotate_quant_kernel<DT, B, 1><<<grid, block, 0, st>>>(x, k, signs, q, s);
-  else if (per_thread <= 2) rotate_quant_kernel<DT, B, 2><<<grid, block, 0, st>>>(x, k, signs, q, s);
-  else if (per_thread <= 3) rotate_quant_kernel<DT, B, 3><<<grid, block, 0, st>>>(x, k, signs, q, s);
-  else if (per_thread <= 4) rotate_quant_kernel<DT, B, 4><<<grid, block, 0, st>>>(x, k, signs, q, s);
-  else if (per_thread <= 8) rotate_quant_kernel<DT, B, 8><<<grid, block, 0, st>>>(x, k, signs, q, s);
+  // One workgroup per row, as wide as gives each thread about two chunks (as for the row
+  // quantizer): at [4096, 16384] H128, 1024 threads x 2 chunks instead of 256 x 8.  A block's
+  // LPB lanes stay inside one wave at every width (chunk c sits on thread c mod KT, and LPB
+  // divides 64).  The row peak is order-independent, so the codes do not depend on the width.
+  const int64_t chunks = k / Shape<B>::EPC;
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (chunks <= 256) rq_launch<DT, B, 1, 256>(grid, x, k, signs, q, s, st);
+  else if (chunks <= 512) rq_launch<DT, B, 2, 256>(grid, x, k, signs, q, s, st);
+  else if (chunks <= 768) rq_launch<DT, B, 3, 256>(grid, x, k, signs, q, s, st);
+  else if (chunks <= 1024) rq_launch<DT, B, 2, 512>(grid, x, k, signs, q, s, st);
+  else if (chunks <= 2048) rq_launch<DT, B, 2, 1024>(grid, x, k, signs, q, s, st);
+  else if (chunks <= 4096) rq_launch<DT, B, 4, 1024>(grid, x, k, signs, q, s, st);
   else {
     set_error("m5k_hadamard_quantize_rows: K=%lld exceeds the register-resident row limit %d", (long long)k,
-              8 * kThreads * Shape<B>::EPC);
+              4 * 1024 * Shape<B>::EPC);
     return M5K_EINVAL;
   }
   return launch_status("m5k_hadamard_quantize_rows");
