@@ -212,11 +212,13 @@ __device__ __forceinline__ uint4 rope_apply(const float (&z)[8], const LaneRope&
   float pu[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) pu[t] = HALF8 ? dpp_move<0x128>(u[t]) : __shfl(u[t], r.src, 16);
+  // With rope_half == 64 every channel of a 128-wide head is rotated (8 lg < 128), so only the
+  // general layout keeps the unrotated lanes' values.
   float y[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const float rotated = __builtin_fmaf(r.sgn, pu[t] * s[t], u[t] * c[t]);
-    y[t] = r.rot ? rotated : u[t];
+    y[t] = HALF8 || r.rot ? rotated : u[t];
   }
   return make_uint4(f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3]), f32x2_to_bf16x2(y[4], y[5]),
                     f32x2_to_bf16x2(y[6], y[7]));
