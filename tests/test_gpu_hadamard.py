@@ -52,8 +52,12 @@ def test_rotate_ffn_down_shape(block, device):
 
 
 @pytest.mark.parametrize("block", [32, 128, 256, 1024])
-@pytest.mark.parametrize("shape", [(7, 5376 // 256 * 256), (3, 4096), (3, 6144), (2, 16384), (5, 1024)])
+@pytest.mark.parametrize(
+    "shape", [(7, 5376 // 256 * 256), (3, 4096), (3, 6144), (2, 16384), (5, 1024), (2, 20480), (1, 32768)]
+)
 def test_fused_rotate_quantize_equals_composition(block, shape, device):
+    """Every register layout of the fused kernel: 256 threads with 1-3 chunks, 512 x 2 and
+    1024 x 2 or 4 chunks per thread, full and ragged rows (K 20480 leaves chunks idle)."""
     if shape[1] % block:
         pytest.skip("K not divisible by block")
     rng = np.random.default_rng(31)
@@ -65,6 +69,15 @@ def test_fused_rotate_quantize_equals_composition(block, shape, device):
     oq, os_ = ref.quantize_reference(ref.c_hadamard_f32(x.float().cpu().numpy(), block, np_of(signs)), "int8")
     np.testing.assert_array_equal(np_of(q), oq)
     np.testing.assert_array_equal(np_of(s), os_)
+
+
+def test_fused_rotate_quantize_row_limit(device):
+    """Rows past the register-resident limit (4096 chunks of 8 at H128) are refused with the
+    library's message, before any launch."""
+    x = torch.zeros((1, 65536), dtype=torch.bfloat16, device=device)
+    signs = torch.ones(65536, dtype=torch.int8, device=device)
+    with pytest.raises(RuntimeError, match="register-resident row limit"):
+        rotate_quantize(x, 128, signs)
 
 
 def test_zero_rows_and_dot_preservation(device):

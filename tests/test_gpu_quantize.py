@@ -42,7 +42,7 @@ def _check(xt, mode):
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
 @pytest.mark.parametrize("kind", ["normal", "zeros", "outliers"])
 @pytest.mark.parametrize("dtype", list(DTYPES))
-@pytest.mark.parametrize("shape", [(7, 256), (3, 5376), (5, 100), (2, 33), (4, 40000)])
+@pytest.mark.parametrize("shape", [(7, 256), (3, 5376), (5, 100), (2, 33), (4, 40000), (3, 24576)])
 def test_quantizer_bit_exact(mode, kind, dtype, shape, device):
     x = _input(kind, shape)
     _check(torch.from_numpy(x).to(device).to(DTYPES[dtype]), mode)
