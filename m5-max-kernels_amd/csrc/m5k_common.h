@@ -252,15 +252,14 @@ __device__ __forceinline__ void encode_i8_div(const float (&x)[N], const I8Scale
 // v_cvt_pk_fp8_f32 equals fp8_e4m3_encode on every finite f32 of magnitude below 464 (all
 // 2.28e9 of them compared on MI355X; |x * hi| <= 448.001 here) and is monotone in the value, so
 // when both products give the same code, fl(x / scale) gives it too.  Otherwise (or for an
-// out-of-range reciprocal) the call's values take the IEEE division, on every lane of the wave,
-// and the same conversion of the quotient; quotients at or above 448 in magnitude saturate first
-// as fp8_e4m3_encode does.  Exact ties of fl(x / scale) are common for 16-bit inputs (an E4M3
-// midpoint has 4 significant bits), so this path runs for a sizeable share of groups; the
-// conversion keeps it at the division's cost.
+// out-of-range reciprocal) the value takes the IEEE division and the same conversion of the
+// quotient; quotients at or above 448 in magnitude saturate first as fp8_e4m3_encode does.
+// Exact ties of fl(x / scale) are common for 16-bit inputs (an E4M3 midpoint has 4
+// significant bits), so the exact chain is taken per byte position of a word, on every lane
+// of the wave at once, only for positions unsettled on some lane.
 template <int N>
 __device__ __forceinline__ void encode_fp8(const float (&x)[N], const I8Scale& s, uint32_t (&out)[N / 4]) {
   const I8Bracket e = i8_bracket(s.inv, s.exact);
-  uint64_t unsettled = e.exact ? ~0ull : 0ull;
 #pragma unroll
   for (int w = 0; w < N / 4; ++w) {
     // word_sel false writes bits [15:0] (first operand in the low byte), true bits [31:16].
@@ -268,25 +267,25 @@ __device__ __forceinline__ void encode_fp8(const float (&x)[N], const I8Scale& s
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * e.lo, x[4 * w + 3] * e.lo, lo, true);
     int hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w] * e.hi, x[4 * w + 1] * e.hi, 0, false);
     hi = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2] * e.hi, x[4 * w + 3] * e.hi, hi, true);
-    unsettled |= __builtin_amdgcn_ballot_w64(lo != hi);
-    out[w] = static_cast<uint32_t>(hi);
-  }
-  if (unsettled) {
-    // The exact chain: the IEEE quotient through the same conversion.  A quotient of magnitude
-    // 448 or more, infinite or NaN enters as 448 with its sign bit, which converts to the
-    // software encoder's saturated code (126 and the sign bit).
-#pragma unroll
-    for (int w = 0; w < N / 4; ++w) {
-      float q[4];
+    uint32_t word = static_cast<uint32_t>(hi);
+    if (e.exact || __builtin_amdgcn_ballot_w64(lo != hi)) {
+      // Some lane of the wave has an unsettled value in this word: each byte position that is
+      // unsettled on any lane takes the exact chain on every lane (on a settled lane it gives
+      // the fast code again).  The exact chain is the IEEE quotient through the same
+      // conversion; a quotient of magnitude 448 or more, infinite or NaN enters as 448 with its
+      // sign bit, which converts to the software encoder's saturated code (126 and the sign).
+      const uint32_t diff = static_cast<uint32_t>(lo ^ hi);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const float z = x[4 * w + b] / s.scale;
-        q[b] = fabsf(z) < 448.0f ? z : copysignf(448.0f, z);
+        if (e.exact || __builtin_amdgcn_ballot_w64(((diff >> (8 * b)) & 0xFFu) != 0)) {
+          const float z = x[4 * w + b] / s.scale;
+          const float q = fabsf(z) < 448.0f ? z : copysignf(448.0f, z);
+          const uint32_t code = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q, q, 0, false)) & 0xFFu;
+          word = (word & ~(0xFFu << (8 * b))) | (code << (8 * b));
+        }
       }
-      int c = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-      c = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], c, true);
-      out[w] = static_cast<uint32_t>(c);
     }
+    out[w] = word;
   }
 }
 
