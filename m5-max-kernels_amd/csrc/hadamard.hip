@@ -123,18 +123,25 @@ void rq_launch(dim3 grid, const void* x, int64_t k, const int8_t* signs, int8_t*
 template <int DT, int B>
 int launch_rotate_quant(const void* x, int64_t rows, int64_t k, const int8_t* signs, int8_t* q, float* s,
                         hipStream_t st) {
-  // One workgroup per row, as wide as gives each thread about two chunks (as for the row
-  // quantizer): at [4096, 16384] H128, 1024 threads x 2 chunks instead of 256 x 8.  A block's
-  // LPB lanes stay inside one wave at every width (chunk c sits on thread c mod KT, and LPB
-  // divides 64).  The row peak is order-independent, so the codes do not depend on the width.
+  // One workgroup per row, as wide as leaves each thread about 32 values: 4 chunks of 8 (256
+  // or 512 threads) or 2 chunks of 16 (B = 1024).  At [4096, 16384] H128 512 x 4 measured
+  // 34.3 us against 38.0 us for 1024 x 2 and 39.8 us for 256 x 8; at K 8192, 256 x 4 19.9 us
+  // against 20.9 us for 512 x 2.  A block's LPB lanes stay inside one wave at every width
+  // (chunk c sits on thread c mod KT, and LPB divides 64).  The row peak is
+  // order-independent, so the codes do not depend on the width.
   const int64_t chunks = k / Shape<B>::EPC;
   const dim3 grid(static_cast<unsigned>(rows));
+  constexpr bool WIDE = Shape<B>::EPC >= 16;
   if (chunks <= 256) rq_launch<DT, B, 1, 256>(grid, x, k, signs, q, s, st);
   else if (chunks <= 512) rq_launch<DT, B, 2, 256>(grid, x, k, signs, q, s, st);
   else if (chunks <= 768) rq_launch<DT, B, 3, 256>(grid, x, k, signs, q, s, st);
-  else if (chunks <= 1024) rq_launch<DT, B, 2, 512>(grid, x, k, signs, q, s, st);
-  else if (chunks <= 2048) rq_launch<DT, B, 2, 1024>(grid, x, k, signs, q, s, st);
-  else if (chunks <= 4096) rq_launch<DT, B, 4, 1024>(grid, x, k, signs, q, s, st);
+  else if (chunks <= 1024) {
+    if constexpr (WIDE) rq_launch<DT, B, 2, 512>(grid, x, k, signs, q, s, st);
+    else rq_launch<DT, B, 4, 256>(grid, x, k, signs, q, s, st);
+  } else if (chunks <= 2048) {
+    if constexpr (WIDE) rq_launch<DT, B, 2, 1024>(grid, x, k, signs, q, s, st);
+    else rq_launch<DT, B, 4, 512>(grid, x, k, signs, q, s, st);
+  } else if (chunks <= 4096) rq_launch<DT, B, 4, 1024>(grid, x, k, signs, q, s, st);
   else {
     set_error("m5k_hadamard_quantize_rows: K=%lld exceeds the register-resident row limit %d", (long long)k,
               4 * 1024 * Shape<B>::EPC);

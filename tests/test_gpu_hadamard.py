@@ -53,10 +53,11 @@ def test_rotate_ffn_down_shape(block, device):
 
 @pytest.mark.parametrize("block", [32, 128, 256, 1024])
 @pytest.mark.parametrize(
-    "shape", [(7, 5376 // 256 * 256), (3, 4096), (3, 6144), (2, 16384), (5, 1024), (2, 20480), (1, 32768)]
+    "shape",
+    [(7, 5376 // 256 * 256), (3, 4096), (3, 6144), (2, 8192), (2, 16384), (5, 1024), (2, 20480), (1, 32768)],
 )
 def test_fused_rotate_quantize_equals_composition(block, shape, device):
-    """Every register layout of the fused kernel: 256 threads with 1-3 chunks, 512 x 2 and
+    """Every register layout of the fused kernel: 256 threads with 1-4 chunks, 512 x 2 or 4 and
     1024 x 2 or 4 chunks per thread, full and ragged rows (K 20480 leaves chunks idle)."""
     if shape[1] % block:
         pytest.skip("K not divisible by block")
