@@ -91,6 +91,49 @@ __device__ __forceinline__ void butterflies(float (&v)[Shape<B>::EPC]) {
   }
 }
 
+// Grouped lane tiles for the streaming rotation: a lane holds G = max(1, B/256) groups of 4
+// consecutive elements, group t at block offset 256t + 4 * (lane mod B/4), so every group of a
+// wave is 1 KiB of contiguous FP32 output.  Strides 1 and 2 stay inside a group, strides
+// 4 .. min(B, 256)/2 are lane exchanges, strides 256 .. B/2 pair group t with group t + s in
+// the same lane: the stride order is the natural one, as in butterflies().
+template <int B>
+struct Grouped {
+  static constexpr int G = B > 256 ? B / 256 : 1;
+  static constexpr int LPB = B > 256 ? 64 : B / 4;
+};
+
+template <int B>
+__device__ __forceinline__ void butterflies_grouped(float (&v)[4 * Grouped<B>::G]) {
+  constexpr int G = Grouped<B>::G;
+#pragma unroll
+  for (int t = 0; t < G; ++t) {
+    float* w = v + 4 * t;
+    const float a0 = w[0] + w[1], a1 = w[0] - w[1], a2 = w[2] + w[3], a3 = w[2] - w[3];
+    w[0] = a0 + a2;
+    w[1] = a1 + a3;
+    w[2] = a0 - a2;
+    w[3] = a1 - a3;
+  }
+  cross_stages<1, Grouped<B>::LPB>(v, static_cast<int>(threadIdx.x & 63));
+#pragma unroll
+  for (int s = 1; s < G; s <<= 1) {
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      if ((t & s) == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float a = v[4 * t + r], c = v[4 * (t + s) + r];
+          v[4 * t + r] = a + c;
+          v[4 * (t + s) + r] = a - c;
+        }
+      }
+    }
+  }
+  constexpr float inv = inv_sqrt_block<B>();
+#pragma unroll
+  for (int r = 0; r < 4 * G; ++r) v[r] = v[r] * inv;
+}
+
 // Per-row INT8 encoder for butterflies<B, false> output z': the reference's rotated value is
 // z = fl(z' * c), c = 1/sqrt(B) in FP32, and its code clamp(rint(fl(z / scale))).  Rounding
 // is monotone, so the row peak max |z| = fl(max |z'| * c); the bracket multipliers come from
