@@ -230,44 +230,5 @@ struct SignMask8 {
   }
 };
 
-// Load EPC consecutive elements of dtype DT starting at element index e (16-byte aligned
-// when the caller checked alignment) and apply the shared signs.
-template <int DT, int EPC>
-__device__ __forceinline__ void load_signed(const void* __restrict__ x, int64_t e, const int8_t* __restrict__ signs,
-                                            int64_t j, float (&v)[EPC]) {
-  constexpr int EB = dtype_bytes<DT>();
-  constexpr int NV = EPC * EB / 16;  // 16-byte vectors
-  const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + e * EB);
-#pragma unroll
-  for (int t = 0; t < NV; ++t) {
-    const uint4 w = p[t];
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if constexpr (DT == M5K_F32) {
-        v[t * 4 + q] = __uint_as_float(ws[q]);
-      } else if constexpr (DT == M5K_BF16) {
-        v[t * 8 + 2 * q] = bf16_bits_to_f32(ws[q] & 0xFFFFu);
-        v[t * 8 + 2 * q + 1] = bf16_bits_to_f32(ws[q] >> 16);
-      } else {
-        v[t * 8 + 2 * q] = f16_bits_to_f32(ws[q] & 0xFFFFu);
-        v[t * 8 + 2 * q + 1] = f16_bits_to_f32(ws[q] >> 16);
-      }
-    }
-  }
-  // Signs are +-1: multiplication is an exact sign flip.
-  const uint2* sp = reinterpret_cast<const uint2*>(signs + j);
-#pragma unroll
-  for (int t = 0; t < EPC / 8; ++t) {
-    const uint2 s = sp[t];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t byte = ((q < 4 ? s.x : s.y) >> (8 * (q & 3))) & 0xFFu;
-      const float sg = static_cast<float>(static_cast<int8_t>(byte));
-      v[t * 8 + q] = v[t * 8 + q] * sg;
-    }
-  }
-}
-
 }  // namespace hadamard
 }  // namespace m5k
