@@ -614,6 +614,71 @@ def settle(torch, fn, seconds):
     return calls
 
 
+VENDOR_SHAPES = [("ffn_down", 4096, 4096, 16384), ("ffn_up", 4096, 16384, 4096), ("q_proj", 4096, 4096, 4096),
+                 ("m9914", 9914, 4096, 4096), ("h3_ffn_up", 4096, 14336, 5376)]
+
+
+def vendor_probe(torch, dev, rounds=8, reps=10):
+    """Our INT8 and FP8 GEMMs against hipBLASLt on the same codes: torch._int_mm (INT32 out, no
+    epilogue) and torch._scaled_mm on the FP8 codes viewed as float8_e4m3fn, with per-row and
+    per-column FP32 scales (the reference's scaling) and with scalar scales.  Inputs as the
+    headline (A ~ N(0,1), W ~ N(0, 0.02), bf16, seed 29) at each shape; ABBA rounds of `reps`
+    launches between one event pair, medians in ms."""
+    from m5kernels_amd import gemm, quantize
+
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    out = []
+    for name, m, n, k in VENDOR_SHAPES:
+        a = torch.randn((m, k), generator=g, device=dev).to(bf)
+        w = (torch.randn((n, k), generator=g, device=dev) * 0.02).to(bf)
+        aq, sa = quantize(a, "int8")
+        wq, ws = quantize(w, "int8")
+        a8, sa8 = quantize(a, "fp8")
+        w8, ws8 = quantize(w, "fp8")
+        wq_t = wq.t()
+        fns = {
+            "m5k_int8": lambda: gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=bf),
+            "hipblaslt_int8": lambda: torch._int_mm(aq, wq_t),
+            "m5k_fp8": lambda: gemm(a8, w8, "fp8", a_scales=sa8, b_scales=ws8, output_dtype=bf),
+        }
+        af, wf = a8.view(torch.float8_e4m3fn), w8.view(torch.float8_e4m3fn)
+        one = torch.ones((), device=dev)
+        sa_col, sb_row = sa8.view(m, 1).float(), ws8.view(1, n).float()
+        for key, fn in (("hipblaslt_fp8_rowwise",
+                         lambda: torch._scaled_mm(af, wf.t(), scale_a=sa_col, scale_b=sb_row, out_dtype=bf)),
+                        ("hipblaslt_fp8_scalar",
+                         lambda: torch._scaled_mm(af, wf.t(), scale_a=one, scale_b=one, out_dtype=bf))):
+            try:
+                fn()
+                fns[key] = fn
+            except Exception as e:  # not every torch build offers every scaling
+                log(f"[bench] vendor probe: {key} unavailable ({str(e).splitlines()[0][:100]})")
+        for fn in fns.values():
+            for _ in range(20):
+                fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = {key: [] for key in fns}
+        names = list(fns)
+        for r in range(rounds):
+            for key in names if r % 2 == 0 else names[::-1]:
+                e0.record()
+                for _ in range(reps):
+                    fns[key]()
+                e1.record()
+                torch.cuda.synchronize()
+                times[key].append(e0.elapsed_time(e1) / reps)
+        ops = 2 * m * n * k
+        row = {"shape": name, "m": m, "n": n, "k": k}
+        for key, v in times.items():
+            ms = statistics.median(v)
+            row[key] = {"ms": ms, "TOPS": ops / (ms * 1e-3) / 1e12}
+        out.append(row)
+        log(f"[bench] vendor probe {name}: " + ", ".join(f"{key} {row[key]['ms'] * 1e3:.1f} us" for key in times))
+    return out
+
+
 def counter_workload(torch, dev, reps):
     """The kernels whose hardware counters the profiles quote, `reps` launches each after a
     clock-settling run, in this order: the FFN-down INT8 GEMM (ours), the same GEMM on constant
@@ -683,6 +748,8 @@ def main():
                    help="only run a 256 MiB device copy x5 (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     p.add_argument("--schedules", action="store_true",
                    help="only compare the library's GEMM schedules (mixed / narrow) with the plain launch")
+    p.add_argument("--vs-hipblaslt", action="store_true",
+                   help="only time the INT8 and FP8 GEMMs against hipBLASLt on five shapes")
     p.add_argument("--counter-workload", type=int, default=0, metavar="REPS",
                    help="only launch each profiled kernel REPS times (for rocprofv3 --pmc runs)")
     p.add_argument("--settle-seconds", type=float, default=0.4,
@@ -713,6 +780,9 @@ def main():
         return
     if args.counter_workload:
         counter_workload(torch, dev, args.counter_workload)
+        return
+    if args.vs_hipblaslt:
+        print(json.dumps({"vs_hipblaslt": vendor_probe(torch, dev)}))
         return
     if args.schedules:
         res = schedules_probe(torch, dev)
