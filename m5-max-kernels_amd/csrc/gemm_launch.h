@@ -127,8 +127,9 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int
           for (int j = 0; j < Geo::FN; ++j)
 #pragma unroll
             for (int e = 0; e < Geo::PER; ++e) {
+              // Entries past M or N are staged unmasked: the write-out below skips them.
               const int r = geo.row(i, e), c = geo.col(j);
-              const float value = (m0 + r < M && n0 + c < N) ? val[j][e] : 0.0f;
+              const float value = val[j][e];
               tile[r * TILE16_STRIDE + c] = static_cast<uint16_t>(
                   GATE != EPI_NONE || OUT_DT == M5K_BF16 ? f32_to_bf16_bits(value) : f32_to_f16_bits(value));
             }

@@ -274,9 +274,10 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
       for (int j = 0; j < Geo::FN; ++j)
 #pragma unroll
         for (int e = 0; e < Geo::PER; ++e) {
+          // Entries past M or N are staged unmasked: no (row, head) pair reads them.
           const int r = geo.row(i, e), c = geo.col(j);
           float value;
-          if constexpr (MODE == I8) value = (m0 + r < M && n0 + c < N) ? (static_cast<float>(acc[i][j][e]) * rs[e]) * cs[j] : 0.0f;
+          if constexpr (MODE == I8) value = (static_cast<float>(acc[i][j][e]) * rs[e]) * cs[j];
           else value = acc[i][j][e];
           tile[r * TILE16_STRIDE + c] = static_cast<uint16_t>(f32_to_bf16_bits(value));
         }
