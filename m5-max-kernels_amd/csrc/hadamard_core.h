@@ -142,6 +142,8 @@ template <int B>
 struct FoldedI8 {
   float scale;
   I8Bracket bracket;
+  FoldedI8() = default;
+  __device__ __forceinline__ FoldedI8(float scale_, const I8Bracket& bracket_) : scale(scale_), bracket(bracket_) {}
   __device__ __forceinline__ explicit FoldedI8(float peak_unscaled) {
     constexpr float c = inv_sqrt_block<B>();
     const I8Scale s = i8_scale(quant_scale<M5K_QUANT_INT8>(peak_unscaled * c));

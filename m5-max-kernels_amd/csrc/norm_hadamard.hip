@@ -136,7 +136,7 @@ __device__ __forceinline__ void load_input8(const PrepParams& p, int64_t row, in
 // inv = 1 / sqrt(var + eps).  Reduction tree: lane partials in chunk order, then the
 // layout's reduction (wave xor-butterfly; for GroupRow the 4 wave sums in order).  Chunks
 // past the row hold zeros and are re-zeroed after centring.
-template <class L, int NV>
+template <class L, int NV, bool VAR_ONLY = false>
 __device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV / 8], bool full,
                                            const PrepParams& p, float* red) {
   const int layer = p.layer;
@@ -167,6 +167,7 @@ __device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV
     for (int i = 0; i < NV; ++i) acc = __builtin_fmaf(v[i], v[i], acc);
     var = div_k(L::sum(acc, red + kWaves), p);  // slot 1
   }
+  if constexpr (VAR_ONLY) return var;
   return 1.0f / sqrtf(var + p.eps);
 }
 
@@ -192,9 +193,12 @@ __device__ __forceinline__ void store_words8_at(uint8_t* row_base, uint32_t col,
 template <int XDT, int PDT, int B, int NCH, bool GATED, int BDT, bool FULL>
 __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int64_t rows) {
   __shared__ float red[3 * kWaves];  // one slot per block reduction
+  __shared__ float row_consts[4];    // inverse, then scale and bracket multipliers (wave 0's)
+  __shared__ int row_exact;
   constexpr int EPC = Shape<B>::EPC;
   constexpr int NV = NCH * EPC;
   constexpr int N8 = NV / 8;  // 8-element groups per lane
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t nchunks = p.k / EPC;
@@ -253,7 +257,15 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[8 * g + i] = t[i];
   }
-  const float inv = row_stats<GroupRow, NV>(v, live, full, p, red);
+  // The row's scalar chains (the square root and division of the inverse, later the scale and
+  // bracket of the encoder) run on wave 0 alone and reach the other waves through the LDS.
+  const float var = row_stats<GroupRow, NV, true>(v, live, full, p, red);
+  if (wave == 0) {
+    const float iv = 1.0f / sqrtf(var + p.eps);
+    if (lane == 0) row_consts[0] = iv;
+  }
+  __syncthreads();
+  const float inv = row_consts[0];
   // Modulation with the signs folded in, then the unscaled butterflies and the row peak:
   // t = O(fma((c * inv) * gs, 1 + sc, hs)), gs and hs the sign-flipped gamma and shift.
   float peak = 0.0f;
@@ -290,8 +302,26 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
       peak = fmaxf(peak, fabsf(z[r]));
     }
   }
-  const hadamard::FoldedI8<B> enc(GroupRow::max(peak, red + 2 * kWaves));  // slot 2
-  if (lane == 0) p.scales[row] = enc.scale;
+  {
+    const float wmax = wave_max(peak);
+    if ((lane & 63) == 0) red[2 * kWaves + wave] = wmax;  // slot 2
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float r = red[2 * kWaves];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) r = fmaxf(r, red[2 * kWaves + w]);
+    const hadamard::FoldedI8<B> e(r);
+    if (lane == 0) {
+      row_consts[1] = e.scale;
+      row_consts[2] = e.bracket.lo;
+      row_consts[3] = e.bracket.hi;
+      row_exact = e.bracket.exact ? 1 : 0;
+      p.scales[row] = e.scale;
+    }
+  }
+  __syncthreads();
+  const hadamard::FoldedI8<B> enc(row_consts[1], I8Bracket{row_consts[2], row_consts[3], row_exact != 0});
   int8_t* qrow = p.q + row * p.k;
 #pragma unroll
   for (int g = 0; g < N8; ++g) {
