@@ -36,6 +36,19 @@ def test_rotate_bit_exact_and_reference_gate(block, dtype, device):
     np.testing.assert_allclose(np_of(y), ref.block_hadamard_reference(x32, block, signs), rtol=2e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("block", [32, 128, 256, 512, 1024])
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_rotate_ragged_grid(block, dtype, device):
+    """37 rows of 2 blocks: the last workgroup's second tile slab ends mid-grid (lanes past the
+    end rotate zeros and store nothing), for 4-element tiles and for grouped tiles (B >= 512)."""
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((37, 2 * block), dtype=np.float32)
+    xt = torch.from_numpy(x).to(device).to(DTYPES[dtype])
+    signs = ref.hadamard_signs(2 * block, 5)
+    y = rotate(xt, block, torch.from_numpy(signs).to(device))
+    np.testing.assert_array_equal(np_of(y), ref.c_hadamard_f32(xt.float().cpu().numpy(), block, signs))
+
+
 @pytest.mark.parametrize("block", [128, 256])
 def test_rotate_ffn_down_shape(block, device):
     g = torch.Generator(device="cpu").manual_seed(29)
