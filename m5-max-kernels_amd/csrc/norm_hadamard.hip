@@ -109,7 +109,6 @@ struct GroupRow {  // one workgroup of 4 wave64 per row
   __device__ static int64_t row() { return blockIdx.x; }
   __device__ static int lane() { return threadIdx.x; }
   __device__ static float sum(float v, float* red) { return block_sum<kWaves>(v, red); }
-  __device__ static float max(float v, float* red) { return block_max<kWaves>(v, red); }
 };
 
 // Row input for 8 elements at column j: X, or the gated residual update rounded to the
