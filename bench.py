@@ -142,27 +142,32 @@ def cpu_model():
     return None
 
 
-def time_op(torch, fn, reps=20, warm=10):
-    """Device time of fn on the current stream.
+def time_op(torch, fn, reps=20, warm=10, settle_s=0.15):
+    """Steady-state device time of fn on the current stream.
 
-    A GPU spin is queued first so the host enqueues every launch before the first one runs:
-    the launches then execute back to back and the events measure device time only, not the
-    Python wrapper's per-call overhead (which exceeds the run time of the smaller kernels).
-    avg_ms comes from one event pair around `reps` back-to-back calls; an event pair around
-    every call adds a few microseconds per call on this device, so the per-call pass only
-    supplies the p10/p90 spread (and its own mean, per_call_avg_ms)."""
+    fn first runs back to back for `settle_s` seconds of device time: MI355X ramps its clocks
+    over the first ~100 ms of sustained load after idle and drops them again in an idle gap of
+    tens of milliseconds.  A short GPU spin (~2 ms) is then queued ahead of the timed launches, so
+    the host enqueues every one of them before the first runs: they execute back to back and the
+    events measure device time only, not the Python wrapper's per-call overhead (which exceeds
+    the run time of the smaller kernels).  With a 50M-cycle spin instead (tens of milliseconds
+    near idle) the FFN-up GEMM measured 270.6 us against 227.3 us settled.  avg_ms comes from one
+    event pair around `reps` back-to-back calls; an event pair around every call adds a few
+    microseconds per call on this device, so the per-call pass only supplies the p10/p90 spread
+    (and its own mean, per_call_avg_ms)."""
     for _ in range(warm):
         fn()
-    torch.cuda.synchronize()
+    settle(torch, fn, settle_s)
     b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(50_000_000)
+    torch.cuda._sleep(5_000_000)
     b0.record()
     for _ in range(reps):
         fn()
     b1.record()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    torch.cuda._sleep(50_000_000)
+    settle(torch, fn, settle_s / 3)
+    torch.cuda._sleep(10_000_000)
     for e0, e1 in evs:
         e0.record()
         fn()
