@@ -142,7 +142,10 @@ def cpu_model():
     return None
 
 
-def time_op(torch, fn, reps=20, warm=10, settle_s=0.15):
+OP_SETTLE_S = 0.15  # device seconds of back-to-back calls before each timed op (--op-settle)
+
+
+def time_op(torch, fn, reps=20, warm=10, settle_s=None):
     """Steady-state device time of fn on the current stream.
 
     fn first runs back to back for `settle_s` seconds of device time: MI355X ramps its clocks
@@ -155,6 +158,7 @@ def time_op(torch, fn, reps=20, warm=10, settle_s=0.15):
     event pair around `reps` back-to-back calls; an event pair around every call adds a few
     microseconds per call on this device, so the per-call pass only supplies the p10/p90 spread
     (and its own mean, per_call_avg_ms)."""
+    settle_s = OP_SETTLE_S if settle_s is None else settle_s
     for _ in range(warm):
         fn()
     settle(torch, fn, settle_s)
@@ -757,9 +761,13 @@ def main():
                    help="only time the INT8 and FP8 GEMMs against hipBLASLt on five shapes")
     p.add_argument("--counter-workload", type=int, default=0, metavar="REPS",
                    help="only launch each profiled kernel REPS times (for rocprofv3 --pmc runs)")
+    p.add_argument("--op-settle", type=float, default=OP_SETTLE_S,
+                   help="device seconds each timed extra runs before timing (0 for counter runs)")
     p.add_argument("--settle-seconds", type=float, default=0.4,
                    help="minimum device time of the warmup, whatever --warmup says (clock ramp)")
     args = p.parse_args()
+    global OP_SETTLE_S
+    OP_SETTLE_S = args.op_settle
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(
