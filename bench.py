@@ -145,6 +145,11 @@ def cpu_model():
 OP_SETTLE_S = 0.15  # device seconds of back-to-back calls before each timed op (--op-settle)
 
 
+def _set_op_settle(seconds):
+    global OP_SETTLE_S
+    OP_SETTLE_S = seconds
+
+
 def time_op(torch, fn, reps=20, warm=10, settle_s=None):
     """Steady-state device time of fn on the current stream.
 
@@ -766,8 +771,7 @@ def main():
     p.add_argument("--settle-seconds", type=float, default=0.4,
                    help="minimum device time of the warmup, whatever --warmup says (clock ramp)")
     args = p.parse_args()
-    global OP_SETTLE_S
-    OP_SETTLE_S = args.op_settle
+    _set_op_settle(args.op_settle)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(
