@@ -295,21 +295,23 @@ def test_fused_prep_bit_exact_vs_fixed_order_oracle(norm, dtype, round_output, b
 @pytest.mark.parametrize("dtype,branch_dtype", [("bf16", "bf16"), ("bf16", "fp32"), ("bf16", "fp16"),
                                                 ("fp16", "bf16"), ("fp32", "bf16"), ("fp16", "fp16")])
 @pytest.mark.parametrize("mapped", [False, True])
-def test_gated_prep_mixed_branch_dtype_bit_exact(norm, dtype, branch_dtype, mapped, device):
+@pytest.mark.parametrize("width", [5376, 4096])
+def test_gated_prep_mixed_branch_dtype_bit_exact(norm, dtype, branch_dtype, mapped, width, device):
     """A branch of another float dtype than the residual: float(branch) enters the FP32 product
     and add as is (norm_hadamard.py:184 accepts any float dtype); R_next, codes and scales equal
-    the fixed-order oracle, and the staged gated_residual_add equals R_next."""
+    the fixed-order oracle, and the staged gated_residual_add equals R_next.  Width 4096 fills
+    every lane's chunks (the full-row instantiation), 5376 leaves lanes idle."""
     rng = np.random.default_rng(401)
-    shape = (7, 5376)
+    shape = (7, width)
     rt = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(device).to(DT[dtype])
     bt = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * 3).to(device).to(DT[branch_dtype])
-    gate = torch.from_numpy(rng.uniform(-0.7, 0.7, size=(3, 5376) if mapped else 5376).astype(np.float32))
+    gate = torch.from_numpy(rng.uniform(-0.7, 0.7, size=(3, width) if mapped else width).astype(np.float32))
     gate = gate.to(device).to(torch.bfloat16)
     gmap = torch.tensor([1, 0, 2, 2, 1, 0, 1], dtype=torch.int32, device=device) if mapped else None
-    gamma = (1 + 0.1 * torch.randn(5376, device=device)).to(torch.bfloat16)
-    scale = (0.1 * torch.randn(5376, device=device)).to(torch.bfloat16)
-    shift = (0.1 * torch.randn(5376, device=device)).to(torch.bfloat16)
-    signs = torch.from_numpy(ref.hadamard_signs(5376, 29)).to(device)
+    gamma = (1 + 0.1 * torch.randn(width, device=device)).to(torch.bfloat16)
+    scale = (0.1 * torch.randn(width, device=device)).to(torch.bfloat16)
+    shift = (0.1 * torch.randn(width, device=device)).to(torch.bfloat16)
+    signs = torch.from_numpy(ref.hadamard_signs(width, 29)).to(device)
     q, s, upd = fused_gated_residual_norm_hadamard_quantize(rt, bt, gate, gamma, scale, shift, signs, 256, norm=norm,
                                                             gate_row_map=gmap)
     assert upd.dtype == rt.dtype
