@@ -7,6 +7,8 @@
 //          path) with one workgroup per row; the rotated row stays in VGPRs between
 //          the row-peak reduction and the encode, so HBM sees 2K + K + 4 bytes per row.
 //          Codes equal the two-kernel composition bit for bit (same FP32 values).
+#include <type_traits>
+
 #include "hadamard_core.h"
 
 namespace m5k {
@@ -86,7 +88,6 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(const void* __restrict
     }
   }
 }
-
 
 // One row per workgroup.  Every load of the row (x and signs of all CPT chunks) is issued
 // before the first wait; a chunk past the row end (only when nchunks is not a multiple of the
