@@ -264,13 +264,17 @@ int launch_quantize(const void* x, int64_t rows, int64_t k, void* q, float* s, h
   // chunks each.  A wider workgroup finishes its row sooner, and at FFN-down ([4096, 16384]
   // BF16, 2048 chunks) 1024 threads x 2 chunks measured 29.4 us against 30.2 us for 512 x 4
   // and 32.0-32.7 us for 256 x 8; at K 4096 (512 chunks) 256 x 2 measured 9.3 us against 15.7
-  // us for 512 x 1.  The row peak is order-independent, so codes and scales do not depend on
-  // the width.
+  // us for 512 x 1.  FP8 rows of up to 2048 chunks take 512 x 4: inside the FP8 online step
+  // (quantize + FP8 GEMM, FFN-down) it measured 232.3 us against 234.5 us for 1024 x 2.  The row
+  // peak is order-independent, so codes and scales do not depend on the width.
   if (!vec) quantize_rows_scalar<DT, MODE><<<grid, block, 0, st>>>(x, k, qb, s);
   else if (chunks <= 256) launch_vec<DT, MODE, 256, 1>(xb, rows, k, qb, s, st);
   else if (chunks <= 512) launch_vec<DT, MODE, 256, 2>(xb, rows, k, qb, s, st);
   else if (chunks <= 1024) launch_vec<DT, MODE, 512, 2>(xb, rows, k, qb, s, st);
-  else if (chunks <= 2048) launch_vec<DT, MODE, 1024, 2>(xb, rows, k, qb, s, st);
+  else if (chunks <= 2048) {
+    if constexpr (MODE == M5K_QUANT_FP8) launch_vec<DT, MODE, 512, 4>(xb, rows, k, qb, s, st);
+    else launch_vec<DT, MODE, 1024, 2>(xb, rows, k, qb, s, st);
+  }
   else if (chunks <= 4096) launch_vec<DT, MODE, 1024, 4>(xb, rows, k, qb, s, st);
   else if (chunks <= 8192) launch_vec<DT, MODE, 1024, 8>(xb, rows, k, qb, s, st);
   else quantize_rows_wide<DT, MODE><<<grid, block, 0, st>>>(xb, k, qb, s);
