@@ -337,18 +337,20 @@ __device__ __forceinline__ void read_frag(const uint8_t* row, int s, int fq, int
 
 // MFMAs of block rows [I0, I1) of fc, with the reads of fn (sub-step s of sa/sb; B fragments
 // first, then A rows in order, as the next sub-step consumes them) spread evenly over those
-// rows.  Scheduling fences keep each read ahead of the MFMA row it is placed before; left
-// alone, the compiler sinks every read next to its first use, which exposes the LDS latency.
-// Measured on the 16 x 16 modes: INT8 +1-4%, BF16 +2-4%; FP8 (two reads per fragment, 253
-// VGPRs) ran 0-4% slower this way and keeps the compiler's order.
-template <int MODE, class G, int I0, int I1>
+// rows, and hook(k) called before row k's reads (the stage DMA uses it).  Scheduling fences keep
+// each read ahead of the MFMA row it is placed before; left alone, the compiler sinks every read
+// next to its first use, which exposes the LDS latency.  Measured on the 16 x 16 modes: INT8
+// +1-4%, BF16 +2-4%; FP8 (two reads per fragment, 253 VGPRs) ran 0-4% slower this way and keeps
+// the compiler's order.
+template <int MODE, class G, int I0, int I1, class H>
 __device__ __forceinline__ void mfma_rows_reading(AccTile<MODE, G>& acc, const FragSet<MODE, G>& fc,
                                                   FragSet<MODE, G>& fn, const uint8_t* sa, const uint8_t* sb,
-                                                  int s, int a_row0, int b_row0, int fq, int fsw) {
+                                                  int s, int a_row0, int b_row0, int fq, int fsw, H&& hook) {
   constexpr int FM = Blk<MODE, G>::FM, FN = Blk<MODE, G>::FN, MD = Blk<MODE, G>::MD;
   constexpr int NR = FM + FN, ROWS = I1 - I0;
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
+    hook(k);
 #pragma unroll
     for (int r = k * NR / ROWS; r < (k + 1) * NR / ROWS; ++r) {
       if (r < FN) read_frag<MODE>(sb + (b_row0 + MD * r) * BKB, s, fq, fsw, fn.b[r]);
@@ -377,8 +379,8 @@ __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 
 //   (16 x 16 modes: the reads are interleaved with the MFMA rows, see mfma_rows_reading)
 //   MFMAs of the last sub-step, first half of the block rows
 //   wait for own stage kt+1 loads and all LDS reads; barrier  (stage kt+1 visible, buffer free)
-//   DMA stage kt+2 into buffer kt & 1
-//   read stage kt+1 sub-step 0 fragments | MFMAs of the last sub-step, second half
+//   read stage kt+1 sub-step 0 fragments | MFMAs of the last sub-step, second half, with the
+//   DMA of stage kt+2 into buffer kt & 1 spread over these MFMA rows
 // Stage kt+1's loads therefore have one whole stage to land, and the barrier sits between MFMA
 // groups, so its latency and the next stage's first LDS reads overlap MFMAs in flight.  Each
 // accumulator sees K in order, sub-step by sub-step.
@@ -433,7 +435,12 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   // window stay out of range.  In the last partial stage of a ragged K (Kb % 128 != 0) the lanes
   // whose chunk starts at or past K set the offset's top bit (out of range: zeros); stages past
   // the range use an empty window.  One VALU op per DMA instruction.
-  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) {
+  //
+  // A stage is NQ instructions, A_0 B_0 A_1 B_1 ... (then the rest of the longer list);
+  // dma_range issues instructions [q0, q1) of stage kr.
+  constexpr int NQ = G::DMA_INSTR + G::DMA_INSTR_B;
+  constexpr int NPAIR = G::DMA_INSTR < G::DMA_INSTR_B ? G::DMA_INSTR : G::DMA_INSTR_B;
+  auto dma_range = [&](uint8_t* sa, uint8_t* sb, int64_t kr, int q0, int q1) {
     const uint32_t kofs = static_cast<uint32_t>((kt_begin + kr) * BKB);
     const uint32_t la = lds_addr(sa) + lds_row0, lb = lds_addr(sb) + lds_row0_b;
     const bool live = kr < kt_count;
@@ -443,10 +450,25 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
     const uint32_t ofs = live ? kofs : 0;
     const v4i ra = window_rsrc(a_win, live ? rec_a : 0, ofs), rb = window_rsrc(b_win, live ? rec_b : 0, ofs);
 #pragma unroll
-    for (int i = 0; i < G::DMA_INSTR; ++i) {
-      dma16(la + 8 * i * BKB, a_base[i] | kill[i & 1], ra);
-      if (i < G::DMA_INSTR_B) dma16(lb + 8 * i * BKB, b_base[i] | kill[i & 1], rb);
+    for (int q = q0; q < q1; ++q) {
+      const bool is_b = q < 2 * NPAIR ? (q & 1) != 0 : G::DMA_INSTR_B > G::DMA_INSTR;
+      const int i = q < 2 * NPAIR ? q >> 1 : q - NPAIR;
+      if (!is_b) dma16(la + 8 * i * BKB, a_base[i] | kill[i & 1], ra);
+      else dma16(lb + 8 * i * BKB, b_base[i] | kill[i & 1], rb);
     }
+  };
+  auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) { dma_range(sa, sb, kr, 0, NQ); };
+  // The DMA of stage kr spread over the ROWS MFMA rows that follow the stage barrier: row k issues
+  // instructions [k NQ / ROWS, (k + 1) NQ / ROWS).  Issued in one burst right after the barrier,
+  // the eight waves' DMA queued behind each other while both waves of every SIMD stalled; spread
+  // two to a row the FFN-down main loop measured 7-10% faster (same bits).
+  auto dma_spread = [&](uint8_t* sa, uint8_t* sb, int64_t kr, auto rows_tag) {
+    constexpr int ROWS = decltype(rows_tag)::value;
+    return [&, sa, sb, kr](int k) {
+#pragma unroll
+      for (int kk = 0; kk < ROWS; ++kk)
+        if (kk == k) dma_range(sa, sb, kr, kk * NQ / ROWS, (kk + 1) * NQ / ROWS);
+    };
   };
 
   int frow, fq, fsw;
@@ -455,13 +477,15 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
 
   FragSet<MODE, G> f0, f1;
 
+  auto no_hook = [](int) {};
   auto stage = [&](auto cur_tag, int64_t kt) {
     constexpr int CUR = decltype(cur_tag)::value, NXT = CUR ^ 1;
+    using Half = std::integral_constant<int, FM - FM / 2>;
 #pragma unroll
     for (int s = 0; s + 1 < SUB; ++s) {
       if constexpr (PIPELINED) {
         mfma_rows_reading<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0, (s & 1) ? f0 : f1, stage_a<CUR>(),
-                                          stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw);
+                                          stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw, no_hook);
       } else {
         read_frags<MODE, G>(stage_a<CUR>(), stage_b<CUR>(), s + 1, a_row0, b_row0, fq, fsw, (s & 1) ? f0 : f1);
         mfma_rows<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0);
@@ -472,11 +496,15 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
     // The DMA below overwrites this buffer: every wave's reads of it must have returned.
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     stage_barrier();
-    dma(stage_a<CUR>(), stage_b<CUR>(), kt + 2);
+    auto hook = dma_spread(stage_a<CUR>(), stage_b<CUR>(), kt + 2, Half{});
     if constexpr (PIPELINED) {
       mfma_rows_reading<MODE, G, FM / 2, FM>(acc, f1, f0, stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq,
-                                             fsw);
+                                             fsw, hook);
     } else {
+      // FP8 / FP32 (32 x 32 blocks, two rows per half) keep one burst: spread over their two rows
+      // the DMA state pushed the FP8 kernels past 256 VGPRs.
+      (void)hook;
+      dma(stage_a<CUR>(), stage_b<CUR>(), kt + 2);
       read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw, f0);
       mfma_rows<MODE, G, FM / 2, FM>(acc, f1);
     }
