@@ -758,12 +758,87 @@ def vendor_probe(torch, dev, rounds=8, reps=10):
     return out
 
 
+def _diag_lib():
+    import ctypes
+
+    from m5kernels_amd import build as hip_build
+
+    if not hip_build.DIAG_LIB_PATH.exists():
+        raise RuntimeError(f"{hip_build.DIAG_LIB_PATH} is missing: build it with `python -m m5kernels_amd.build`")
+    lib = ctypes.CDLL(str(hip_build.DIAG_LIB_PATH))
+    lib.m5k_diag_mfma_ceiling.restype = ctypes.c_int
+    lib.m5k_diag_mfma_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                          ctypes.c_void_p]
+    return lib
+
+
+def ceiling_kernels(torch, dev, aq, wq):
+    """name -> launcher of the MFMA ceiling kernels (libm5k_diag.so) on the FFN-down codes: the
+    GEMM main loop's v_mfma_i32_16x16x64_i8 stream alone, register-resident fragments read from
+    the bench's own A and W codes, K / 128 iterations = the GEMM's MFMA count; the same on
+    constant codes (all 1); and the v_mfma_i32_32x32x32_i8 form of the same work."""
+    import ctypes
+
+    lib = _diag_lib()
+    out = torch.empty((M // 256) * (N // 256) * 512, dtype=torch.int32, device=dev)
+
+    def launcher(md, constant):
+        def run():
+            stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+            rc = lib.m5k_diag_mfma_ceiling(aq.data_ptr(), wq.data_ptr(), M, N, K, K // 128, constant, md,
+                                           out.data_ptr(), stream)
+            if rc != 0:
+                raise RuntimeError(f"m5k_diag_mfma_ceiling failed ({rc})")
+        return run
+
+    return {"mfma_ceiling_16x16x64": launcher(16, 0), "mfma_ceiling_16x16x64_constant": launcher(16, 1),
+            "mfma_ceiling_32x32x32": launcher(32, 0)}
+
+
+def mfma_ceiling(torch, dev, rounds=8, reps=10):
+    """--mfma-ceiling: the FFN-down INT8 GEMM beside the MFMA-only ceiling kernels on its own codes
+    (ceiling_kernels), ABBA rounds of `reps` launches between one event pair after a 0.4 s clock
+    settle; medians.  gemm_frac_of_ceiling = ceiling time / GEMM time."""
+    from m5kernels_amd import gemm, quantize
+
+    a, w = make_inputs(torch, dev)
+    wq, ws = quantize(w, "int8")
+    aq, sa = quantize(a, "int8")
+    del a, w
+    fns = {"gemm_i8": lambda: gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)}
+    fns.update(ceiling_kernels(torch, dev, aq, wq))
+    settle(torch, fns["gemm_i8"], 0.4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = {key: [] for key in fns}
+    names = list(fns)
+    for r in range(rounds):
+        for key in names if r % 2 == 0 else names[::-1]:
+            e0.record()
+            for _ in range(reps):
+                fns[key]()
+            e1.record()
+            torch.cuda.synchronize()
+            times[key].append(e0.elapsed_time(e1) / reps)
+    ops = 2.0 * M * N * K
+    res = {"workload": "ffn_down_w8a8 codes (bench inputs)", "m": M, "n": N, "k": K, "rounds": rounds, "reps": reps}
+    for key, v in times.items():
+        ms = statistics.median(v)
+        tops = ops / (ms * 1e-3) / 1e12
+        res[key] = {"us": ms * 1e3, "TOPS": tops, "frac_of_int8_peak": tops / PEAK_INT8_TOPS,
+                    "p10_p90_us": [sorted(v)[len(v) // 10] * 1e3, sorted(v)[(9 * len(v)) // 10] * 1e3]}
+        log(f"[bench] mfma ceiling: {key} {ms * 1e3:.1f} us = {tops:.0f} TOPS ({tops / PEAK_INT8_TOPS:.3f})")
+    res["gemm_frac_of_ceiling"] = res["mfma_ceiling_16x16x64"]["us"] / res["gemm_i8"]["us"]
+    return res
+
+
 def counter_workload(torch, dev, reps):
     """The kernels whose hardware counters the profiles quote, `reps` launches each after a
     clock-settling run, in this order: the FFN-down INT8 GEMM (ours), the same GEMM on constant
     codes, hipBLASLt's INT8 GEMM (torch._int_mm) on the bench's codes, the FFN-down FP8 GEMM,
     the INT8 and FP8 quantizers on
-    the FFN-down activation, the fused gated and ungated prep (M 4096, K 4096, H128) and the
+    the FFN-down activation, the MFMA ceiling kernels on the same codes (ceiling_kernels), the fused
+    gated and ungated prep (M 4096, K 4096, H128) and the
     RMS quantizer (M 4096, K 4096, H256).  For rocprofv3 --pmc runs; prints nothing else."""
     from m5kernels_amd import (fused_gated_residual_norm_hadamard_quantize, fused_norm_hadamard_quantize, gemm,
                                quantize, rms_quantize)
@@ -788,6 +863,7 @@ def counter_workload(torch, dev, reps):
         ("quantize_int8", lambda: quantize(a, "int8")),
         ("quantize_fp8", lambda: quantize(a, "fp8")),
     ]
+    runs += list(ceiling_kernels(torch, dev, aq, wq).items())
     g = torch.Generator(device=dev).manual_seed(SEED)
     m, k, tables = 4096, 4096, 2
     res = torch.randn((m, k), generator=g, device=dev).to(bf)
@@ -829,6 +905,8 @@ def main():
                    help="only compare the library's GEMM schedules (mixed / narrow) with the plain launch")
     p.add_argument("--vs-hipblaslt", action="store_true",
                    help="only time the INT8 and FP8 GEMMs against hipBLASLt on five shapes")
+    p.add_argument("--mfma-ceiling", action="store_true",
+                   help="only time the FFN-down GEMM beside MFMA-only kernels on its own codes (the ceiling)")
     p.add_argument("--counter-workload", type=int, default=0, metavar="REPS",
                    help="only launch each profiled kernel REPS times (for rocprofv3 --pmc runs)")
     p.add_argument("--op-settle", type=float, default=OP_SETTLE_S,
@@ -859,6 +937,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log("[bench] copied 256 MiB x5")
+        return
+    if args.mfma_ceiling:
+        print(json.dumps({"mfma_ceiling": mfma_ceiling(torch, dev)}))
         return
     if args.counter_workload:
         counter_workload(torch, dev, args.counter_workload)

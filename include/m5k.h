@@ -136,9 +136,11 @@ int m5k_gemm_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, i
  * the process ends), so the call allocates nothing -- no hipMalloc, no hipFree, no allocating
  * library routine.  No counterpart in the reference: it is for callers that cannot allocate
  * (HIP graph capture, tight serving loops, harnesses that forbid allocation).
- * splits * m * n must not exceed M5K_SCRATCH_ELEMS (M5K_EINVAL otherwise).  Every call on one
- * GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
- * threads) race.  Results are bit-identical to m5k_gemm_i8_splitk and m5k_gemm_i8.
+ * splits * m * n must not exceed M5K_SCRATCH_ELEMS (M5K_EINVAL otherwise).  The array used is
+ * the one on the device of `stream` (the current device for the null stream); its address is
+ * looked up once per device, the first call on that device.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other host threads) race.  Results
+ * are bit-identical to m5k_gemm_i8_splitk and m5k_gemm_i8.
  */
 #define M5K_SCRATCH_ELEMS (16 * 1024 * 1024)
 int m5k_gemm_i8_splitk_noalloc(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t k,
@@ -162,6 +164,18 @@ int m5k_gemm_i8_splitk_noalloc(const int8_t* a, const int8_t* b, int64_t m, int6
  * the environment switch schedule 1 / 2 off.
  */
 int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus, int* schedule, int64_t* full_tiles);
+
+/*
+ * Force the schedule of the MFMA GEMM launches made by the calling host thread: -1 restores the
+ * library's own plan (m5k_gemm_launch_plan), 0 plain, 1 mixed, 2 narrow (plain for FP8/FP32).
+ * *previous (may be NULL) receives the thread's earlier setting.  No counterpart in the
+ * reference, whose tuner searches Metal threadgroup tiles through gemm's `tile` argument
+ * (src/m5kernels/cli.py:66-151); this is the gfx950 knob the harness tuner searches instead.
+ * The setting is thread-local, so other host threads keep their own plan; for tools outside the
+ * process, M5K_GEMM_SCHEDULE=plain|mixed|narrow in the environment does the same when no thread
+ * setting is made.  Results are bit-identical under every schedule.
+ */
+int m5k_gemm_set_schedule(int schedule, int* previous);
 
 /*
  * Raw INT32 accumulators of the W8A8 GEMM (test hook for bit-exact parity):

@@ -60,6 +60,15 @@ extern "C" int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus,
   return M5K_OK;
 }
 
+extern "C" int m5k_gemm_set_schedule(int schedule, int* previous) {
+  clear_error();
+  M5K_REQUIRE(schedule >= -1 && schedule <= SCHED_NARROW, "m5k_gemm_set_schedule: schedule %d outside [-1, 2]",
+              schedule);
+  if (previous) *previous = g_thread_schedule;
+  g_thread_schedule = schedule;
+  return M5K_OK;
+}
+
 namespace {
 
 // Split-K partials of m5k_gemm_i8_splitk_noalloc.  The name is a host-side stand-in: host code
@@ -70,15 +79,25 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 int32_t* g_scratch[kMaxDevices] = {};
 
-// This GPU's copy of `scratch` (looked up once per device, with that device current).
-int scratch_of_current_device(int32_t** out, const char* name) {
-  int dev = -1;
-  M5K_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, "%s: no current HIP device (%d)",
-              name, dev);
+// The copy of `scratch` on the device that `stream` belongs to (the current device for the null
+// stream), looked up once per device with that device current and cached.
+int scratch_of_stream_device(hipStream_t stream, int32_t** out, const char* name) {
+  int current = -1;
+  M5K_REQUIRE(hipGetDevice(&current) == hipSuccess && current >= 0, "%s: no current HIP device", name);
+  int dev = current;
+  if (stream != nullptr) {
+    hipDevice_t sd = -1;
+    const hipError_t e = hipStreamGetDevice(stream, &sd);
+    M5K_REQUIRE(e == hipSuccess, "%s: hipStreamGetDevice failed: %s", name, hipGetErrorString(e));
+    dev = static_cast<int>(sd);
+  }
+  M5K_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device %d outside the supported range", name, dev);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch[dev] == nullptr) {
+    if (dev != current) M5K_REQUIRE(hipSetDevice(dev) == hipSuccess, "%s: hipSetDevice(%d) failed", name, dev);
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != current) (void)hipSetDevice(current);
     M5K_REQUIRE(e == hipSuccess && ptr != nullptr, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name,
                 dev, hipGetErrorString(e));
     g_scratch[dev] = static_cast<int32_t*>(ptr);
@@ -131,7 +150,7 @@ extern "C" int m5k_gemm_i8_splitk_noalloc(const int8_t* a, const int8_t* b, int6
               "%s: splits*m*n = %lld INT32 partials exceed the %d-element scratch array", name,
               (long long)(static_cast<int64_t>(splits) * m * n), M5K_SCRATCH_ELEMS);
   int32_t* ws = nullptr;
-  if (int rc = scratch_of_current_device(&ws, name)) return rc;
+  if (int rc = scratch_of_stream_device(as_stream(stream), &ws, name)) return rc;
   // Every partial that the epilogue reads is written first by the split kernel, so the
   // array needs no clearing between calls.
   const int rc = m5k_gemm_i8_splitk(a, b, m, n, k, a_scales, b_scales, c, c_dtype, bias, bias_row_map, residual, gate,

@@ -115,7 +115,7 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int
     };
 
     // 16-bit outputs: stage the rounded tile (the BF16 branch for the gated form) in the LDS the
-    // main loop has released, then write whole 512-byte tile rows with 16-byte stores.
+    // main loop has released, then write whole 512-byte tile rows with 16-byte streaming stores.
     if constexpr (OUT_DT == M5K_BF16 || OUT_DT == M5K_F16) {
       if (p.coalesced) {
         uint16_t* tile = reinterpret_cast<uint16_t*>(g_lds);
@@ -159,7 +159,7 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int
             }
             w = make_uint4(out[0], out[1], out[2], out[3]);
           }
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + idx) = w;
+          store_stream16(static_cast<uint16_t*>(p.c) + idx, w);
         }
         return;
       }
@@ -333,16 +333,26 @@ inline bool dma_ok(const void* a, const void* b, int64_t kb) {
 
 enum Schedule { SCHED_PLAIN = 0, SCHED_MIXED = 1, SCHED_NARROW = 2 };
 
-// A schedule named by M5K_GEMM_SCHEDULE ("plain", "mixed", "narrow"; read on every call, for
-// tuners that measure each one), or -1.  A forced mixed launch keeps the planner's full-tile
-// count when it has one, else runs every tile of the last (or only) round as two halves.
+// A schedule forced for the calls of this host thread (m5k_gemm_set_schedule: the harness tuner),
+// else one named by M5K_GEMM_SCHEDULE ("plain", "mixed", "narrow"; read on every call, for outside
+// tools), else -1.  A forced mixed launch keeps the planner's full-tile count when it has one, else
+// runs every tile of the last (or only) round as two halves.
+inline thread_local int g_thread_schedule = -1;
+
 inline int forced_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& full) {
-  const char* env = std::getenv("M5K_GEMM_SCHEDULE");
-  if (env == nullptr || env[0] == '\0') return -1;
+  int which = g_thread_schedule;
+  if (which < 0) {
+    const char* env = std::getenv("M5K_GEMM_SCHEDULE");
+    if (env == nullptr || env[0] == '\0') return -1;
+    if (std::strcmp(env, "plain") == 0) which = SCHED_PLAIN;
+    else if (std::strcmp(env, "mixed") == 0) which = SCHED_MIXED;
+    else if (std::strcmp(env, "narrow") == 0) which = SCHED_NARROW;
+    else return -1;
+  }
   full = -1;
-  if (std::strcmp(env, "plain") == 0) return SCHED_PLAIN;
-  if (std::strcmp(env, "narrow") == 0) return md16 ? SCHED_NARROW : SCHED_PLAIN;
-  if (std::strcmp(env, "mixed") == 0 && cus >= XCDS && cus % XCDS == 0) {
+  if (which == SCHED_PLAIN) return SCHED_PLAIN;
+  if (which == SCHED_NARROW) return md16 ? SCHED_NARROW : SCHED_PLAIN;
+  if (which == SCHED_MIXED && cus >= XCDS && cus % XCDS == 0) {
     const int64_t total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     full = mixed_full_tiles(m, n, cus);
     if (full < 0) full = total > cus ? (total - 1) / cus * cus : 0;

@@ -93,7 +93,7 @@ __device__ __forceinline__ void norm_rope_16(const float (&z)[8], Partner partne
     else packed[t >> 1] = bits;
   }
   uint16_t* out = p.y + (static_cast<int64_t>(head) * m_rows + row) * HEAD + 8 * lg;
-  *reinterpret_cast<uint4*>(out) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  store_stream16(out, make_uint4(packed[0], packed[1], packed[2], packed[3]));
 }
 
 // Fast path for rope_half % 8 == 0 (R = 48 and 64 included): a lane's 8 channels are either
@@ -332,17 +332,17 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
         if (h >= heads_here) continue;
         const int k = HPT * i + h;
         const BlockDst d = block_dst(p, n0 / HEAD + h);  // uniform across the group
-        uint4* dst = reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg);
+        uint16_t* dst = d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg;
         if (d.gamma == nullptr) {  // V: the rounded projection
-          *dst = w[k];
+          store_stream16(dst, w[k]);
           continue;
         }
         float z[8];
         unpack8_bf16(w[k], z);
         const LaneRope& rr = d.gamma == p.gamma ? lr : lrk;
         const float inv = row16_bcast(inv_mine, k);
-        *dst = p.rope_half == 64 ? rope_apply<true>(z, rr, cw[i], sw[i], inv)
-                                 : rope_apply<false>(z, rr, cw[i], sw[i], inv);
+        store_stream16(dst, p.rope_half == 64 ? rope_apply<true>(z, rr, cw[i], sw[i], inv)
+                                              : rope_apply<false>(z, rr, cw[i], sw[i], inv));
       }
     }
     return;
@@ -355,8 +355,8 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
     const uint16_t* src = tile + local_row * TILE16_STRIDE + local_head * HEAD;
     const BlockDst d = block_dst(p, block);
     if (d.gamma == nullptr) {
-      *reinterpret_cast<uint4*>(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg) =
-          *reinterpret_cast<const uint4*>(src + 8 * lg);
+      store_stream16(d.out + (static_cast<int64_t>(d.head) * M + row) * HEAD + 8 * lg,
+                     *reinterpret_cast<const uint4*>(src + 8 * lg));
       continue;
     }
     QkParams ps = p;
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
     lane_cos_sin(p, lr, row, lg, cw, sw);
     const uint4 out = p.rope_half == 64 ? norm_rope_fast<true>(z, lr, cw, sw, p.eps)
                                         : norm_rope_fast<false>(z, lr, cw, sw, p.eps);
-    *reinterpret_cast<uint4*>(p.y + (static_cast<int64_t>(head) * M + row) * HEAD + 8 * lg) = out;
+    store_stream16(p.y + (static_cast<int64_t>(head) * M + row) * HEAD + 8 * lg, out);
     return;
   }
   norm_rope_16(z, [&](int d) { return bf16_bits_to_f32(src[d]); }, p, row, M, head, lg);

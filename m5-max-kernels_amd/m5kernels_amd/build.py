@@ -1,7 +1,8 @@
 """Build libm5k.so (gfx950 HIP kernels + C ABI) in-tree with hipcc.
 
 Every translation unit under ``csrc/`` is compiled to an object under ``_build/``
-(in parallel), then linked into ``lib/libm5k.so`` next to this package.  Flags:
+(in parallel), then linked into ``lib/libm5k.so`` next to this package.  The measurement
+kernels under ``diag/`` (bench.py's MFMA ceiling) go into ``lib/libm5k_diag.so``.  Flags:
 
 * ``--offload-arch=gfx950`` only: MI355X is the single target.
 * ``-ffp-contract=off``: no FMA contraction, so FP32 epilogues and normalization keep
@@ -26,6 +27,8 @@ CSRC = PKG_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 BUILD_DIR = REPO_ROOT / "_build" / "libm5k"
 LIB_PATH = PKG_ROOT / "lib" / "libm5k.so"
+DIAG_DIR = PKG_ROOT / "diag"
+DIAG_LIB_PATH = PKG_ROOT / "lib" / "libm5k_diag.so"
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -82,9 +85,21 @@ def build(force: bool = True, jobs: int | None = None, verbose: bool = False) ->
     if proc.returncode != 0:
         raise RuntimeError(f"link of libm5k.so failed:\n{proc.stderr[-4000:]}")
     os.replace(tmp, LIB_PATH)
+    build_diag()
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB_PATH} from {len(srcs)} sources, and {DIAG_LIB_PATH}", file=sys.stderr)
     return LIB_PATH
+
+
+def build_diag() -> Path:
+    """Link lib/libm5k_diag.so: measurement kernels used by bench.py (no op uses them)."""
+    tmp = DIAG_LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-shared", "-o", str(tmp), *map(str, sorted(DIAG_DIR.glob("*.hip")))]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build of libm5k_diag.so failed:\n{proc.stderr[-4000:]}")
+    os.replace(tmp, DIAG_LIB_PATH)
+    return DIAG_LIB_PATH
 
 
 if __name__ == "__main__":

@@ -159,31 +159,35 @@ SCHEDULES = ("plain", "mixed", "narrow")
 _override = threading.local()
 
 
+_SCHEDULE_CODES = {name: i for i, name in enumerate(SCHEDULES)}
+
+
 @contextlib.contextmanager
 def launch_override(schedule=None, splits=None):
-    """Fix the gfx950 GEMM launch for the calls made inside the block: `schedule` ("plain",
-    "mixed" or "narrow", read by the library from M5K_GEMM_SCHEDULE on every call) and, for
-    the W8A8 linear, the split-K count `splits` (1: no split; the INT32 partials are exact, so
-    every choice gives the same bits).  None keeps the library's own plan.  These are the knobs
-    the harness tuner searches; the environment variable is process-wide, so the block is meant
-    for one thread at a time."""
+    """Fix the gfx950 GEMM launch for the calls this thread makes inside the block: `schedule`
+    ("plain", "mixed" or "narrow"; set in the library for this host thread with
+    m5k_gemm_set_schedule) and, for the W8A8 linear, the split-K count `splits` (1: no split;
+    the INT32 partials are exact, so every choice gives the same bits).  A forced schedule with
+    `splits` None runs unsplit: the launch timed is the one named.  None keeps the library's own
+    plan.  These are the knobs the harness tuner searches; both settings are thread-local."""
     if schedule is not None and schedule not in SCHEDULES:
         raise ValueError(f"unknown GEMM schedule {schedule!r}")
     if splits is not None and (isinstance(splits, bool) or not isinstance(splits, int) or not 1 <= splits <= 64):
         raise ValueError("splits must be an integer in [1, 64]")
-    saved_env = os.environ.get("M5K_GEMM_SCHEDULE")
+    saved_schedule = getattr(_override, "schedule", None)
     saved_splits = getattr(_override, "splits", None)
+    previous = ctypes.c_int(-1)
     if schedule is not None:
-        os.environ["M5K_GEMM_SCHEDULE"] = schedule
+        _lib.call("m5k_gemm_set_schedule", _SCHEDULE_CODES[schedule], ctypes.byref(previous))
+        _override.schedule = schedule
     _override.splits = splits
     try:
         yield
     finally:
         _override.splits = saved_splits
-        if saved_env is None:
-            os.environ.pop("M5K_GEMM_SCHEDULE", None)
-        else:
-            os.environ["M5K_GEMM_SCHEDULE"] = saved_env
+        if schedule is not None:
+            _lib.call("m5k_gemm_set_schedule", previous.value, None)
+            _override.schedule = saved_schedule
 
 
 def launch_plan(mode, m, n, cus=256):
@@ -209,6 +213,8 @@ def _i8_schedule(m, n, k, cus, env):
     schedule switches `env` (M5K_GEMM_MIXED_TILES, M5K_GEMM_NARROW_TILES, M5K_GEMM_SCHEDULE):
     (splits, tail), with
     tail = (rows of the plain launch, splits of the rest) or None."""
+    if env[2]:
+        return 1, None  # a schedule forced from the environment runs unsplit, as named
     splits = splitk_plan(m, n, k, cus)
     # The library's mixed and narrow launches refill a partial last round without INT32
     # partials and measured faster wherever both apply; the split-K tail takes the rest.
@@ -339,6 +345,8 @@ def gemm(
         forced_splits = getattr(_override, "splits", None)
         if aligned and forced_splits is not None:
             splits = forced_splits
+        elif aligned and getattr(_override, "schedule", None) is not None:
+            splits = 1  # a forced schedule runs unsplit, without the tail split
         elif aligned:
             env = tuple(os.environ.get(v) for v in ("M5K_GEMM_MIXED_TILES", "M5K_GEMM_NARROW_TILES", "M5K_GEMM_SCHEDULE"))
             splits, tail = _i8_schedule(m, n, k, _cu_count(a.device), env)

@@ -224,18 +224,15 @@ def test_tune_launch_space():
         assert cli.Launch.from_record(launch.record()) == launch
 
 
-def test_launch_override_sets_and_restores(monkeypatch):
-    import os
-
+def test_launch_override_sets_and_restores():
     from m5kernels_amd import hip
 
-    monkeypatch.delenv("M5K_GEMM_SCHEDULE", raising=False)
     with hip.launch_override("narrow", 4):
-        assert os.environ["M5K_GEMM_SCHEDULE"] == "narrow" and hip._override.splits == 4
+        assert hip._override.schedule == "narrow" and hip._override.splits == 4
         with hip.launch_override(None, None):
-            assert os.environ["M5K_GEMM_SCHEDULE"] == "narrow" and hip._override.splits is None
+            assert hip._override.schedule == "narrow" and hip._override.splits is None
         assert hip._override.splits == 4
-    assert "M5K_GEMM_SCHEDULE" not in os.environ and hip._override.splits is None
+    assert getattr(hip._override, "schedule", None) is None and hip._override.splits is None
     with pytest.raises(ValueError):
         with hip.launch_override("diagonal"):
             pass
@@ -248,10 +245,9 @@ def _fake_run_case(times, calls):
     """A stand-in for engine.run_case: records the call and the launch in force, and times
     each launch by `times` (None: incorrect)."""
     from m5kernels_amd import hip
-    import os
 
     def run_case(c, backend, precision, seed=17, distribution="normal", warmup=3, repeat=10, tile=(64, 64, 4, 1)):
-        launch = cli.Launch(os.environ.get("M5K_GEMM_SCHEDULE"), getattr(hip._override, "splits", None))
+        launch = cli.Launch(getattr(hip._override, "schedule", None), getattr(hip._override, "splits", None))
         calls.append((c["id"], backend, precision, seed, launch))
         ms = times.get(launch, 1.0) if backend != "mlx" else 2.0
         if ms is None:

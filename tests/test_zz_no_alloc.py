@@ -67,3 +67,29 @@ def test_noalloc_rejects_sizes_beyond_the_scratch_array(device):
     splits = SCRATCH_ELEMS // (m * n) + 1
     with pytest.raises(RuntimeError, match="scratch array"):
         _call("m5k_gemm_i8_splitk_noalloc", a, b, sa, sb, extra, splits, torch.bfloat16)
+
+
+def test_noalloc_replays_under_graph_capture(device):
+    """The use the header names: a warm-up call (the per-device scratch lookup happens there),
+    then the call captured in a HIP graph and replayed, with eager work between replays; every
+    replay must equal the workspace form bit for bit."""
+    m, n, k, splits = 128, 1536, 5376, 3
+    a, b, sa, sb, extra = _operands(m, n, k, 4, device, "bias")
+    want = _call("m5k_gemm_i8_splitk", a, b, sa, sb, extra, splits, torch.float32)
+    c = torch.empty((m, n), dtype=torch.float32, device=device)
+    args = [_lib.ptr(a), _lib.ptr(b), m, n, k, _lib.ptr(sa), _lib.ptr(sb), _lib.ptr(c), _lib.dtype_code(c),
+            _lib.ptr(extra["bias"]), None, None, None, None, splits]
+    _lib.call("m5k_gemm_i8_splitk_noalloc", *args, _lib.stream_of(a))
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int32), want.view(torch.int32))
+    graph, side = torch.cuda.CUDAGraph(), torch.cuda.Stream(device=device)
+    with torch.cuda.graph(graph, stream=side):
+        _lib.call("m5k_gemm_i8_splitk_noalloc", *args, _lib.stream_of(a))
+    other = _operands(256, 2048, 1024, 5, device, "plain")
+    for _ in range(3):
+        c.fill_(float("nan"))
+        _call("m5k_gemm_i8_splitk_noalloc", *other, 4, torch.bfloat16)  # eager use of the scratch between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c.view(torch.int32), want.view(torch.int32))
