@@ -14,8 +14,10 @@ Timing.  After the W warmup steps, further untimed steps run until at least --se
 (0.4 s) of device time has passed, whatever W is: on MI355X the first ~100 steps after idle run
 10-15% slower while the clocks ramp (the count is reported as settle_steps).  The headline region has
 only a start and an end event around the K steps (per-step timing events add ~3%); a second
-pass of K steps with an event pair around each kernel gives the per-kernel durations that the
-roofline uses.
+pass of K steps gives the per-kernel durations that the roofline uses: each kernel records its
+own start and end into a pair of events (m5k_time_next_launch).  Events recorded between the
+kernels would add their own packets, and default ones would write back and invalidate the caches
+between the quantizer and the GEMM, which changes both.
 
 --schedules prints instead one JSON line comparing, on the shapes of SCHEDULE_SHAPES, the GEMM
 schedule the library picks (mixed 256 x 256 + 256 x 128 tiles, or 256 x 224 tiles) with the
@@ -46,6 +48,51 @@ TRAFFIC_FILE = REPO / "profiles" / "traffic.json"
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+class FenceFreeEvent:
+    """A HIP timing event created with hipEventDisableSystemFence (through the HIP runtime torch
+    has loaded).  torch.cuda.Event records with a system-scope release, which writes back and
+    invalidates the caches between the kernels it separates: in the FFN-down step that moved
+    ~15 us of the quantizer's and the GEMM's cache write-back into the wrong interval (the event
+    pass summed to 231.6 us against a 214.5 us step; the rocprof kernel trace of an event-free
+    step agreed with neither).  Without the fence the event only timestamps the stream."""
+
+    _hip = None
+    DISABLE_SYSTEM_FENCE = 0x20000000  # hipEventDisableSystemFence (hip_runtime_api.h)
+
+    def __init__(self):
+        import ctypes
+
+        if FenceFreeEvent._hip is None:
+            hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime already loaded by torch (same SONAME)
+            hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            FenceFreeEvent._hip = hip
+        self._ctypes = ctypes
+        self.handle = ctypes.c_void_p()
+        rc = FenceFreeEvent._hip.hipEventCreateWithFlags(ctypes.byref(self.handle), self.DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self, stream):
+        rc = FenceFreeEvent._hip.hipEventRecord(self.handle, self._ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end):
+        ms = self._ctypes.c_float()
+        rc = FenceFreeEvent._hip.hipEventElapsedTime(self._ctypes.byref(ms), self.handle, end.handle)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        hip = getattr(FenceFreeEvent, "_hip", None) if FenceFreeEvent is not None else None
+        if hip is not None and self.handle:
+            hip.hipEventDestroy(self.handle)
 
 
 def make_inputs(torch, dev):
@@ -926,7 +973,7 @@ def main():
 
     import torch
 
-    from m5kernels_amd import gemm, quantize
+    from m5kernels_amd import _lib, gemm, quantize
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -965,28 +1012,40 @@ def main():
     steps = args.steps
     # Timing events exist before the warmup: the first creation in a process costs tens of ms.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    ev = [[FenceFreeEvent() for _ in range(4)] for _ in range(steps)]
     log(f"[bench] warmup {args.warmup} steps, then at least {args.settle_seconds} s of steps; timing {steps} steps")
+    # Each step's output is released before the next step runs, as in the reference's timing loop
+    # (engine.py:70-92: `y = fn()` builds a lazy MLX graph, dropping the previous output, before
+    # mx.eval computes the new one).  Kept alive across the next step, the 32 MB output alternates
+    # between two allocator blocks and the working set outgrows the 256 MB Infinity Cache: 12 us
+    # more per step (rocprof: GEMM +8.5 us, quantizer +3.8 us).
+    y = None
     for _ in range(args.warmup):
+        y = None
         y = step()
     torch.cuda.synchronize()
     settle_steps = settle(torch, step, args.settle_seconds)  # ends synchronized
     t0 = time.perf_counter()
     start.record()
     for i in range(steps):
+        y = None
         y = step()
     end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     total_ms = start.elapsed_time(end)
-    # Per-kernel durations: the same K steps again, an event pair around each kernel.
+    # Per-kernel durations: the same K steps again, each kernel recording its own start and end
+    # into a pair of events (m5k_time_next_launch: hipExtLaunchKernel on the launch stream), so no
+    # event packet sits between the quantizer and the GEMM.
     log(f"[bench] per-kernel pass, {steps} steps")
+    hook = _lib.load().m5k_time_next_launch
     for i in range(steps):
-        ev[i][0].record()
+        y = None
+        hook(ev[i][0].handle, ev[i][1].handle)
         aq, sa = quantize(a, "int8")
-        ev[i][1].record()
+        hook(ev[i][2].handle, ev[i][3].handle)
         y = gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
-        ev[i][2].record()
+        hook(None, None)
     torch.cuda.synchronize()
     quant_ms = [e[0].elapsed_time(e[1]) for e in ev]
     host = []
@@ -996,7 +1055,7 @@ def main():
         torch.cuda.synchronize()
         host.append((time.perf_counter() - h0) * 1e3)
     host.sort()
-    gemm_ms = [e[1].elapsed_time(e[2]) for e in ev]
+    gemm_ms = [e[2].elapsed_time(e[3]) for e in ev]
     ms_per_step = max(total_ms, wall_ms) / steps
     ops = 2.0 * M * N * K
     tops = ops / (ms_per_step * 1e-3) / 1e12
@@ -1067,8 +1126,9 @@ def main():
             "event_total_ms": total_ms,
             "wall_ms": wall_ms,
             "method": ("after the warmup, K steps between one pair of HIP events on the launch stream; value uses "
-                       "max(event, host wall); per-kernel averages come from a second pass of K steps with an "
-                       "event pair around each kernel"),
+                       "max(event, host wall); per-kernel averages come from a second pass of K steps in which each "
+                       "kernel records its own start and end into a pair of events (m5k_time_next_launch, "
+                       "hipExtLaunchKernel), with no event packet between the kernels"),
             "host_sync_ms_per_step": {"median": host[len(host) // 2], "p10": host[len(host) // 10],
                                       "p90": host[(9 * len(host)) // 10]},
             "gemm_p10_p90_ms": [sorted(gemm_ms)[steps // 10], sorted(gemm_ms)[(9 * steps) // 10]],

@@ -393,20 +393,20 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
       if (sched == SCHED_NARROW) {
         using G = Grid8Narrow;
         const int64_t wgs = ((m + BM - 1) / BM) * ((n + G::TN - 1) / G::TN);
-        gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW, G><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(
-            A, B, (int)m, (int)n, kb, q);
+        launch_kernel(gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW, G>, dim3(static_cast<unsigned>(wgs)), block, st,
+                      A, B, (int)m, (int)n, kb, q);
         return launch_status(name);
       }
     }
     if (sched == SCHED_MIXED) {
       const int64_t wgs = full + 2 * (tiles - full);
-      gemm_mixed_kernel<MODE, OUT_DT, BIAS, GATE, RAW><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(
-          A, B, (int)m, (int)n, kb, static_cast<int>(full), q);
+      launch_kernel(gemm_mixed_kernel<MODE, OUT_DT, BIAS, GATE, RAW>, dim3(static_cast<unsigned>(wgs)), block, st, A, B,
+                    (int)m, (int)n, kb, static_cast<int>(full), q);
     } else {
-      gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
+      launch_kernel(gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW>, grid, block, st, A, B, (int)m, (int)n, kb, q);
     }
   } else
-    gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW><<<grid, block, 0, st>>>(A, B, (int)m, (int)n, kb, q);
+    launch_kernel(gemm_kernel<MODE, false, OUT_DT, BIAS, GATE, RAW>, grid, block, st, A, B, (int)m, (int)n, kb, q);
   return launch_status(name);
 }
 

@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void mx_to_bf16_kernel(const int8_t* __re
 
 template <int DT, int MODE, int KT, int CPT>
 void launch_vec(const uint8_t* x, int64_t rows, int64_t k, uint8_t* q, float* s, hipStream_t st) {
-  quantize_rows_vec<DT, MODE, CPT, KT><<<dim3(static_cast<unsigned>(rows)), dim3(KT), 0, st>>>(x, k, q, s);
+  launch_kernel(quantize_rows_vec<DT, MODE, CPT, KT>, dim3(static_cast<unsigned>(rows)), dim3(KT), st, x, k, q, s);
 }
 
 template <int DT, int MODE>
