@@ -170,12 +170,13 @@ __device__ __forceinline__ float row_stats(float (&v)[NV], const bool (&live)[NV
   return 1.0f / sqrtf(var + p.eps);
 }
 
+// R_next's 8 values at column col, written with streaming stores (the row is not read back).
 template <int DT>
 __device__ __forceinline__ void store_words8_at(uint8_t* row_base, uint32_t col,
                                                 const uint32_t (&w)[8 * dtype_bytes<DT>() / 4]) {
-  uint4* q = reinterpret_cast<uint4*>(row_base + col * static_cast<uint32_t>(dtype_bytes<DT>()));
-  q[0] = make_uint4(w[0], w[1], w[2], w[3]);
-  if constexpr (DT == M5K_F32) q[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  uint8_t* q = row_base + col * static_cast<uint32_t>(dtype_bytes<DT>());
+  store_stream16(q, make_uint4(w[0], w[1], w[2], w[3]));
+  if constexpr (DT == M5K_F32) store_stream16(q + 16, make_uint4(w[4], w[5], w[6], w[7]));
 }
 
 // Fused kernel: one row per workgroup of 4 wave64, NCH chunks of EPC elements per lane
