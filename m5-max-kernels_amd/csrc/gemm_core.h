@@ -374,16 +374,20 @@ __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 
 // rows, so both halves of an L2 line are requested by one instruction.  Rows past M/N and
 // chunks past K read as zero through out-of-range buffer offsets.
 //
-// Two stage buffers.  Per stage kt (buffer kt & 1, SUB sub-steps):
-//   read sub-step s+1 fragments | MFMAs of sub-step s            (s < SUB - 1)
-//   (16 x 16 modes: the reads are interleaved with the MFMA rows, see mfma_rows_reading)
-//   MFMAs of the last sub-step, first half of the block rows
+// Two stage buffers.  Per stage kt (buffer kt & 1, SUB sub-steps), 16 x 16 modes:
+//   read sub-step s+1 fragments | MFMAs of sub-step s            (s < SUB - 1; the reads are
+//                                                                 interleaved with the MFMA rows,
+//                                                                 see mfma_rows_reading)
 //   wait for own stage kt+1 loads and all LDS reads; barrier  (stage kt+1 visible, buffer free)
-//   read stage kt+1 sub-step 0 fragments | MFMAs of the last sub-step, second half, with the
-//   DMA of stage kt+2 into buffer kt & 1 spread over these MFMA rows
-// Stage kt+1's loads therefore have one whole stage to land, and the barrier sits between MFMA
-// groups, so its latency and the next stage's first LDS reads overlap MFMAs in flight.  Each
-// accumulator sees K in order, sub-step by sub-step.
+//   read stage kt+1 sub-step 0 fragments | MFMAs of the last sub-step, with the DMA of stage
+//   kt+2 into buffer kt & 1 spread over all of its MFMA rows
+// The barrier thus sits between sub-steps: the next stage's first fragments and the DMA have a
+// whole sub-step of MFMAs to hide behind.  Against a barrier after half of the last sub-step's
+// rows (its reads and DMA over the other half), this measured 1.4-1.6% faster at K = 16384 and
+// at FFN-up (N = 16384, K = 4096), equal at 4096^3, same bits.  The 32 x 32 modes (FP8, FP32)
+// keep the barrier after half of the last sub-step, with the DMA in one burst.
+// Stage kt+1's loads have one whole stage to land.  Each accumulator sees K in order, sub-step
+// by sub-step.
 //
 // The loop covers the 128-byte K stages [kt_begin, kt_begin + kt_count); a split-K launch
 // gives each workgroup one such range (stages past the range, like chunks past K, load zeros).
@@ -461,7 +465,7 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   // The DMA of stage kr spread over the ROWS MFMA rows that follow the stage barrier: row k issues
   // instructions [k NQ / ROWS, (k + 1) NQ / ROWS).  Issued in one burst right after the barrier,
   // the eight waves' DMA queued behind each other while both waves of every SIMD stalled; spread
-  // two to a row the FFN-down main loop measured 7-10% faster (same bits).
+  // over the rows the FFN-down main loop measured 7-10% faster (same bits).
   auto dma_spread = [&](uint8_t* sa, uint8_t* sb, int64_t kr, auto rows_tag) {
     constexpr int ROWS = decltype(rows_tag)::value;
     return [&, sa, sb, kr](int k) {
@@ -480,7 +484,6 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   auto no_hook = [](int) {};
   auto stage = [&](auto cur_tag, int64_t kt) {
     constexpr int CUR = decltype(cur_tag)::value, NXT = CUR ^ 1;
-    using Half = std::integral_constant<int, FM - FM / 2>;
 #pragma unroll
     for (int s = 0; s + 1 < SUB; ++s) {
       if constexpr (PIPELINED) {
@@ -491,19 +494,22 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
         mfma_rows<MODE, G, 0, FM>(acc, (s & 1) ? f1 : f0);
       }
     }
-    mfma_rows<MODE, G, 0, FM / 2>(acc, f1);
-    wait_stage<0>();
-    // The DMA below overwrites this buffer: every wave's reads of it must have returned.
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    stage_barrier();
-    auto hook = dma_spread(stage_a<CUR>(), stage_b<CUR>(), kt + 2, Half{});
     if constexpr (PIPELINED) {
-      mfma_rows_reading<MODE, G, FM / 2, FM>(acc, f1, f0, stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq,
-                                             fsw, hook);
+      wait_stage<0>();
+      // The DMA below overwrites this buffer: every wave's reads of it must have returned.
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      stage_barrier();
+      auto hook = dma_spread(stage_a<CUR>(), stage_b<CUR>(), kt + 2, std::integral_constant<int, FM>{});
+      mfma_rows_reading<MODE, G, 0, FM>(acc, f1, f0, stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw,
+                                        hook);
     } else {
-      // FP8 / FP32 (32 x 32 blocks, two rows per half) keep one burst: spread over their two rows
-      // the DMA state pushed the FP8 kernels past 256 VGPRs.
-      (void)hook;
+      // FP8 / FP32 (32 x 32 blocks, two rows per half): half of the last sub-step's rows before the
+      // barrier, and the DMA in one burst (spread over their rows, the DMA state pushed the FP8
+      // kernels past 256 VGPRs).
+      mfma_rows<MODE, G, 0, FM / 2>(acc, f1);
+      wait_stage<0>();
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      stage_barrier();
       dma(stage_a<CUR>(), stage_b<CUR>(), kt + 2);
       read_frags<MODE, G>(stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw, f0);
       mfma_rows<MODE, G, FM / 2, FM>(acc, f1);
