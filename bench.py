@@ -433,6 +433,40 @@ def _prep_case(torch, dev, m, k=4096, tables=2):
     }
 
 
+def prep_mixed(torch, dev, reps):
+    """--prep-mixed REPS: the C4 gated prep (M 4096, K 4096, LayerNorm, H128, two tables) with a BF16
+    residual, an FP16 branch and the tables in three dtypes (gamma FP16, scale FP32, shift BF16,
+    gate FP32), REPS calls after the inputs are made, then the same call on all-BF16 inputs
+    (time_op each).  Under a rocprofv3 kernel trace the mixed calls are REPS dispatches of the one
+    prep kernel and nothing else: no cast kernels."""
+    from m5kernels_amd import fused_gated_residual_norm_hadamard_quantize
+
+    m, k, tables = 4096, 4096, 2
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    res = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+    branch = torch.randn((m, k), generator=g, device=dev).to(torch.float16)
+    gate = (torch.randn((tables, k), generator=g, device=dev) * 0.1).to(torch.float32)
+    scale = (torch.randn((tables, k), generator=g, device=dev) * 0.1).to(torch.float32)
+    shift = (torch.randn((tables, k), generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn((k,), generator=g, device=dev)).to(torch.float16)
+    row_map = (torch.arange(m, device=dev, dtype=torch.int32) * tables // m).to(torch.int32)
+    signs = torch.ones(k, dtype=torch.int8, device=dev)
+    kw = dict(norm="layer", epsilon=1e-5, round_output="input", row_map=row_map, gate_row_map=row_map)
+    bf = [t.to(torch.bfloat16) for t in (branch, gate, gamma, scale)]
+    torch.cuda.synchronize()
+    log(f"[bench] prep mixed dtypes: {reps} calls")
+    for _ in range(reps):
+        fused_gated_residual_norm_hadamard_quantize(res, branch, gate, gamma, scale, shift, signs, 128, **kw)
+    torch.cuda.synchronize()
+    mixed = time_op(torch, lambda: fused_gated_residual_norm_hadamard_quantize(
+        res, branch, gate, gamma, scale, shift, signs, 128, **kw))
+    same = time_op(torch, lambda: fused_gated_residual_norm_hadamard_quantize(
+        res, bf[0], bf[1], bf[2], bf[3], shift, signs, 128, **kw))
+    return {"m": m, "k": k, "calls": reps, "mixed_dtypes_ms": mixed["avg_ms"], "all_bf16_ms": same["avg_ms"],
+            "dtypes": {"residual": "bf16", "branch": "fp16", "gamma": "fp16", "scale": "fp32", "shift": "bf16",
+                       "gate": "fp32"}}
+
+
 def _qk_case(torch, dev, m=9914, k=4096, n=4096):
     """Q projection + per-head RMSNorm + split-half RoPE (R = 64, base 10000, positions 0..m-1),
     head-major BF16 [32, m, 128]: INT8 online (quantize + fused projection) and BF16 modes, and
@@ -952,6 +986,8 @@ def main():
                    help="only compare the library's GEMM schedules (mixed / narrow) with the plain launch")
     p.add_argument("--vs-hipblaslt", action="store_true",
                    help="only time the INT8 and FP8 GEMMs against hipBLASLt on five shapes")
+    p.add_argument("--prep-mixed", type=int, default=0, metavar="REPS",
+                   help="REPS mixed-dtype gated prep calls (one dispatch each), then their timing; prints nothing else")
     p.add_argument("--mfma-ceiling", action="store_true",
                    help="only time the FFN-down GEMM beside MFMA-only kernels on its own codes (the ceiling)")
     p.add_argument("--counter-workload", type=int, default=0, metavar="REPS",
@@ -987,6 +1023,9 @@ def main():
         return
     if args.mfma_ceiling:
         print(json.dumps({"mfma_ceiling": mfma_ceiling(torch, dev)}))
+        return
+    if args.prep_mixed:
+        print(json.dumps({"prep_mixed": prep_mixed(torch, dev, args.prep_mixed)}))
         return
     if args.counter_workload:
         counter_workload(torch, dev, args.counter_workload)

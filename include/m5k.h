@@ -51,6 +51,13 @@ extern "C" {
 #define M5K_QUANT_FP8 1  /* OCP E4M3 codes in uint8, scale = peak/448 */
 
 /* Normalization kinds for the fused prep. */
+/* Prep parameter-table dtypes (param_dtype of m5k_norm_hadamard_quantize and m5k_norm_modulate):
+ * one float dtype code for every table, or one code per table packed by M5K_PARAM_TABLES (the
+ * gate field is ignored by calls without a gate). */
+#define M5K_PARAM_PER_TABLE 0x100
+#define M5K_PARAM_TABLES(gamma, scale, shift, gate) \
+  (M5K_PARAM_PER_TABLE | (gamma) | ((scale) << 2) | ((shift) << 4) | ((gate) << 6))
+
 #define M5K_NORM_RMS 0
 #define M5K_NORM_LAYER 1
 
@@ -237,12 +244,13 @@ int m5k_hadamard_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t
  * fused_gated_residual_norm_hadamard_quantize (src/m5kernels/norm_hadamard.py:122-265,
  * shaders/norm_hadamard.metal:1-121).
  *   x: [rows,k] of x_dtype (the residual when gated); k % block == 0.
- *   gated: branch [rows,k] of branch_dtype (x_dtype, or F32 for a branch of another float
- *          dtype, widened exactly by the caller), gate [k] or [P,k] with gate_row_map[rows];
- *          residual_out[rows,k] (x_dtype) receives R(x + branch*gate), written once.
- *          branch_dtype is ignored when branch is NULL.
- *   gamma [k]; scale/shift [k], or [P,k] tables selected by row_map[rows]; gamma, scale,
- *   shift and gate share param_dtype (BF16 or F32).  signs int8 [k].
+ *   gated: branch [rows,k] of branch_dtype (BF16, F16 or F32, independent of x_dtype, read as
+ *          is), gate [k] or [P,k] with gate_row_map[rows]; residual_out[rows,k] (x_dtype)
+ *          receives R(x + branch*gate), written once.  branch_dtype is ignored when branch is
+ *          NULL.
+ *   gamma [k]; scale/shift [k], or [P,k] tables selected by row_map[rows]; param_dtype gives
+ *   the tables' dtypes: one float code for all, or M5K_PARAM_TABLES(gamma, scale, shift,
+ *   gate).  signs int8 [k].
  *   norm: M5K_NORM_RMS / M5K_NORM_LAYER; round_to_input: 1 rounds the modulated value to
  *   x_dtype before the signs (round_output="input"), 0 keeps FP32.
  *   Outputs: q int8 [rows,k], scales float32 [rows].
@@ -267,8 +275,8 @@ int m5k_norm_modulate(const void* x, int x_dtype, int64_t rows, int64_t k, const
 /*
  * Staged gated residual update out = R(float(residual) + float(branch) * float(gate)).
  * Replaces norm_hadamard.gated_residual_add (src/m5kernels/norm_hadamard.py:280-300,
- * shaders/gated_residual.metal:1-9).  gate [k] or [P,k] with gate_row_map[rows]; branch of
- * branch_dtype: the residual dtype, or F32 for a branch of another float dtype.
+ * shaders/gated_residual.metal:1-9).  gate [k] or [P,k] of gate_dtype with gate_row_map[rows];
+ * branch of branch_dtype; both BF16, F16 or F32, independent of the residual dtype.
  */
 int m5k_gated_residual_add(const void* residual, int dtype, int64_t rows, int64_t k, const void* branch,
                            int branch_dtype, const void* gate, int gate_dtype, const int32_t* gate_row_map,

@@ -232,5 +232,59 @@ struct SignMask8 {
   }
 };
 
+// Parameter tables of the prep kernels (gamma, scale, shift, gate), 8 columns at a time.
+// Tables<M5K_BF16> reads every table as BF16 (compile-time layout).  Tables<M5K_PMIX> reads each
+// table in its own dtype, given at run time (BF16, FP16 or FP32; wave-uniform, so the choice is a
+// scalar branch), into FP32-sized storage.  Every decode to FP32 is exact, so the FP32 arithmetic
+// that follows sees the same values whatever dtype a table has.
+constexpr int M5K_PMIX = 8;  // template code for per-table run-time dtypes (not an element dtype)
+
+template <int PDT>
+struct Tables;
+
+template <>
+struct Tables<M5K_BF16> {
+  using raw = Raw8<M5K_BF16>;
+  __device__ static raw fetch(const void* base, int64_t e, int) { return fetch8<M5K_BF16>(base, e); }
+  __device__ static void decode(const raw& r, int, float (&v)[8]) { decode8<M5K_BF16>(r, v); }
+  __device__ static raw sign(const raw& r, const uint2& s, int) { return SignMask8<M5K_BF16>(s).apply(r); }
+  __device__ static void load(const void* base, int64_t e, int, float (&v)[8]) { decode8<M5K_BF16>(fetch8<M5K_BF16>(base, e), v); }
+};
+
+template <>
+struct Tables<M5K_PMIX> {
+  using raw = Raw8<M5K_F32>;  // FP32: both words; BF16 / FP16: the first word
+  __device__ static raw fetch(const void* base, int64_t e, int dt) {
+    if (dt == M5K_F32) return fetch8<M5K_F32>(base, e);
+    raw r;
+    r.w[0] = fetch8<M5K_BF16>(base, e).w[0];  // 8 two-byte elements
+    r.w[1] = make_uint4(0u, 0u, 0u, 0u);
+    return r;
+  }
+  __device__ static void decode(const raw& r, int dt, float (&v)[8]) {
+    if (dt == M5K_F32) {
+      decode8<M5K_F32>(r, v);
+    } else if (dt == M5K_BF16) {
+      Raw8<M5K_BF16> h;
+      h.w[0] = r.w[0];
+      decode8<M5K_BF16>(h, v);
+    } else {
+      Raw8<M5K_F16> h;
+      h.w[0] = r.w[0];
+      decode8<M5K_F16>(h, v);
+    }
+  }
+  // BF16 and FP16 keep their sign bits in the same positions (bits 15 and 31 of each word).
+  __device__ static raw sign(const raw& r, const uint2& s, int dt) {
+    if (dt == M5K_F32) return SignMask8<M5K_F32>(s).apply(r);
+    Raw8<M5K_BF16> h;
+    h.w[0] = r.w[0];
+    raw out = r;
+    out.w[0] = SignMask8<M5K_BF16>(s).apply(h).w[0];
+    return out;
+  }
+  __device__ static void load(const void* base, int64_t e, int dt, float (&v)[8]) { decode(fetch(base, e, dt), dt, v); }
+};
+
 }  // namespace hadamard
 }  // namespace m5k

@@ -38,19 +38,20 @@ using hadamard::fetch8;
 using hadamard::fetch8_at;
 using hadamard::Raw8;
 using hadamard::Shape;
-using hadamard::SignMask8;
+using hadamard::M5K_PMIX;
+using hadamard::Tables;
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
 struct PrepParams {
   const void* x;          // residual or X [rows, k] (XDT)
-  const void* branch;     // [rows, k] (XDT) or null: ungated
-  const void* gate;       // [k] or [P, k] (PDT)
+  const void* branch;     // [rows, k] (BDT) or null: ungated
+  const void* gate;       // [k] or [P, k] (dt_gate)
   const int32_t* gate_map;
-  const void* gamma;      // [k] (PDT)
-  const void* scale;      // [k] or [P, k] (PDT)
-  const void* shift;      // [k] or [P, k] (PDT)
+  const void* gamma;      // [k] (dt_gamma)
+  const void* scale;      // [k] or [P, k] (dt_scale)
+  const void* shift;      // [k] or [P, k] (dt_shift)
   const int32_t* row_map;
   const int8_t* signs;    // [k]
   int8_t* q;              // [rows, k]
@@ -62,6 +63,8 @@ struct PrepParams {
   int layer;              // 1: LayerNorm, 0: RMS
   int round_input;        // 1: O = XDT, 0: O = FP32
   float inv_k;            // 1/K when K is a power of two (exact), else 0
+  // Table dtypes (M5K_BF16 / M5K_F16 / M5K_F32), read by the Tables<M5K_PMIX> kernels.
+  int dt_gamma, dt_scale, dt_shift, dt_gate;
 };
 
 // sum / K for the row statistics: the IEEE quotient, or the same value as a multiply by the
@@ -121,7 +124,7 @@ __device__ __forceinline__ void load_input8(const PrepParams& p, int64_t row, in
   if constexpr (GATED) {
     float b[8], g[8];
     load8<BDT>(p.branch, e, b);
-    load8<PDT>(p.gate, goff + j, g);
+    Tables<PDT>::load(p.gate, goff + j, p.dt_gate, g);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = v[i] + b[i] * g[i];
     uint32_t w[8 * dtype_bytes<XDT>() / 4];
@@ -181,8 +184,8 @@ __device__ __forceinline__ void store_words8_at(uint8_t* row_base, uint32_t col,
 
 // Fused kernel: one row per workgroup of 4 wave64, NCH chunks of EPC elements per lane
 // (chunk c = tid + 256 i); FULL when every chunk of every lane lies in the row.  Every global load of the row (X, branch, gate, gamma, scale, shift,
-// signs) is issued up front, so a row waits for memory once.  BDT is the branch dtype: XDT, or
-// FP32 for a branch of another float dtype (the host widens BF16/FP16 branches exactly).
+// signs) is issued up front, so a row waits for memory once.  BDT is the branch dtype (any of
+// BF16, FP16, FP32, read as is); PDT the parameter tables' (Tables).
 //
 // The signs fold into gamma and shift as sign-bit flips of their words:
 // fma((c * inv) * (g * s), 1 + sc, sh * s) = s * fma((c * inv) * g, 1 + sc, sh) for s = +-1,
@@ -216,7 +219,8 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
   const uint8_t* xrow = static_cast<const uint8_t*>(p.x) + row * p.k * dtype_bytes<XDT>();
   Raw8<XDT> xr[N8];
   Raw8<BDT> br[GATED ? N8 : 1];
-  Raw8<PDT> gr[GATED ? N8 : 1], gam[N8], scl[N8], shf[N8];
+  using T = Tables<PDT>;
+  typename T::raw gr[GATED ? N8 : 1], gam[N8], scl[N8], shf[N8];
   uint2 sgn[N8];
 #pragma unroll
   for (int g = 0; g < N8; ++g) {
@@ -224,11 +228,11 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
       xr[g] = fetch8_at<XDT>(xrow, col[g]);
       if constexpr (GATED) {
         br[g] = fetch8_at<BDT>(static_cast<const uint8_t*>(p.branch) + row * p.k * dtype_bytes<BDT>(), col[g]);
-        gr[g] = fetch8<PDT>(p.gate, goff + col[g]);
+        gr[g] = T::fetch(p.gate, goff + col[g], p.dt_gate);
       }
-      gam[g] = fetch8<PDT>(p.gamma, col[g]);
-      scl[g] = fetch8<PDT>(p.scale, toff + col[g]);
-      shf[g] = fetch8<PDT>(p.shift, toff + col[g]);
+      gam[g] = T::fetch(p.gamma, col[g], p.dt_gamma);
+      scl[g] = T::fetch(p.scale, toff + col[g], p.dt_scale);
+      shf[g] = T::fetch(p.shift, toff + col[g], p.dt_shift);
       sgn[g] = *reinterpret_cast<const uint2*>(p.signs + col[g]);
     }
   }
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
       if constexpr (GATED) {
         float b[8], gt[8];
         decode8<BDT>(br[g], b);
-        decode8<PDT>(gr[g], gt);
+        T::decode(gr[g], p.dt_gate, gt);
 #pragma unroll
         for (int i = 0; i < 8; ++i) t[i] = t[i] + b[i] * gt[i];
         uint32_t w[8 * dtype_bytes<XDT>() / 4];
@@ -277,11 +281,10 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
       const int g = ci * (EPC / 8) + h;
       float t[8];
       if (live[g]) {
-        const SignMask8<PDT> mask(sgn[g]);
         float gs[8], sc[8], hs[8];
-        decode8<PDT>(mask.apply(gam[g]), gs);
-        decode8<PDT>(scl[g], sc);
-        decode8<PDT>(mask.apply(shf[g]), hs);
+        T::decode(T::sign(gam[g], sgn[g], p.dt_gamma), p.dt_gamma, gs);
+        T::decode(scl[g], p.dt_scale, sc);
+        T::decode(T::sign(shf[g], sgn[g], p.dt_shift), p.dt_shift, hs);
 #pragma unroll
         for (int i = 0; i < 8; ++i) t[i] = __builtin_fmaf(v[8 * g + i] * inv * gs[i], 1.0f + sc[i], hs[i]);
         if (p.round_input) {
@@ -341,9 +344,9 @@ __global__ __launch_bounds__(kThreads) void fused_prep_kernel(PrepParams p, int6
 template <int PDT>
 __device__ __forceinline__ void modulate8(const PrepParams& p, int64_t toff, int64_t j, float inv, float (&v)[8]) {
   float g[8], sc[8], sh[8];
-  load8<PDT>(p.gamma, j, g);
-  load8<PDT>(p.scale, toff + j, sc);
-  load8<PDT>(p.shift, toff + j, sh);
+  Tables<PDT>::load(p.gamma, j, p.dt_gamma, g);
+  Tables<PDT>::load(p.scale, toff + j, p.dt_scale, sc);
+  Tables<PDT>::load(p.shift, toff + j, p.dt_shift, sh);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(v[i] * inv * g[i], 1.0f + sc[i], sh[i]);
 }
@@ -412,9 +415,10 @@ template <int XDT, int PDT, int B, int NCH, bool GATED, int BDT>
 int launch_prep(const PrepParams& p, int64_t rows, hipStream_t st) {
   // Rows that fill every lane's chunks (K = NCH * 256 * EPC, e.g. K 4096 at B <= 512) take the
   // FULL variant, whose lanes carry no liveness tests or zeroed stand-ins: 3-4% faster at
-  // M 4096 / 9914, K 4096 (identical outputs).  FP32 residuals keep the general kernel only.
+  // M 4096 / 9914, K 4096 (identical outputs).  FP32 residuals, and branches of another dtype
+  // than the residual, keep the general kernel only.
   const dim3 grid(static_cast<unsigned>(rows)), block(kThreads);
-  if constexpr (XDT != M5K_F32) {
+  if constexpr (XDT != M5K_F32 && BDT == XDT) {
     if (p.k == static_cast<int64_t>(NCH) * kThreads * Shape<B>::EPC) {
       fused_prep_kernel<XDT, PDT, B, NCH, GATED, BDT, true><<<grid, block, 0, st>>>(p, rows);
       return launch_status("m5k_norm_hadamard_quantize");
@@ -451,20 +455,23 @@ int fused_by_block(int block, const PrepParams& p, int64_t rows, hipStream_t st)
   }
 }
 
-// branch_dtype is XDT or M5K_F32 (checked by the entry point).
+// branch_dtype is BF16, FP16 or FP32 (checked by the entry point), read as is.
 template <int XDT, int PDT>
 int fused_dispatch(int block, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
   if (!p.branch) return fused_by_block<XDT, PDT, false>(block, p, rows, st);
-  if constexpr (XDT != M5K_F32) {
-    if (branch_dtype == M5K_F32) return fused_by_block<XDT, PDT, true, M5K_F32>(block, p, rows, st);
+  if (branch_dtype == XDT) return fused_by_block<XDT, PDT, true>(block, p, rows, st);
+  switch (branch_dtype) {
+    case M5K_BF16: return fused_by_block<XDT, PDT, true, M5K_BF16>(block, p, rows, st);
+    case M5K_F16: return fused_by_block<XDT, PDT, true, M5K_F16>(block, p, rows, st);
+    default: return fused_by_block<XDT, PDT, true, M5K_F32>(block, p, rows, st);
   }
-  return fused_by_block<XDT, PDT, true>(block, p, rows, st);
 }
 
+// Every table BF16: the compile-time BF16 kernels; otherwise each table in its own dtype.
 template <int XDT>
-int fused_by_param(int pdt, int block, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
-  return pdt == M5K_BF16 ? fused_dispatch<XDT, M5K_BF16>(block, branch_dtype, p, rows, st)
-                         : fused_dispatch<XDT, M5K_F32>(block, branch_dtype, p, rows, st);
+int fused_by_param(bool all_bf16, int block, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
+  return all_bf16 ? fused_dispatch<XDT, M5K_BF16>(block, branch_dtype, p, rows, st)
+                  : fused_dispatch<XDT, M5K_PMIX>(block, branch_dtype, p, rows, st);
 }
 
 template <int XDT, int PDT>
@@ -485,8 +492,8 @@ int launch_norm(const PrepParams& p, int64_t rows, hipStream_t st) {
 }
 
 template <int XDT>
-int norm_by_param(int pdt, const PrepParams& p, int64_t rows, hipStream_t st) {
-  return pdt == M5K_BF16 ? launch_norm<XDT, M5K_BF16>(p, rows, st) : launch_norm<XDT, M5K_F32>(p, rows, st);
+int norm_by_param(bool all_bf16, const PrepParams& p, int64_t rows, hipStream_t st) {
+  return all_bf16 ? launch_norm<XDT, M5K_BF16>(p, rows, st) : launch_norm<XDT, M5K_PMIX>(p, rows, st);
 }
 
 template <int XDT, int PDT, int BDT>
@@ -499,17 +506,18 @@ int launch_gate(const PrepParams& p, int64_t rows, hipStream_t st) {
 }
 
 template <int XDT, int BDT>
-int gate_by_param(int pdt, const PrepParams& p, int64_t rows, hipStream_t st) {
-  return pdt == M5K_BF16 ? launch_gate<XDT, M5K_BF16, BDT>(p, rows, st) : launch_gate<XDT, M5K_F32, BDT>(p, rows, st);
+int gate_by_param(bool bf16_gate, const PrepParams& p, int64_t rows, hipStream_t st) {
+  return bf16_gate ? launch_gate<XDT, M5K_BF16, BDT>(p, rows, st) : launch_gate<XDT, M5K_PMIX, BDT>(p, rows, st);
 }
 
-// branch_dtype is XDT or M5K_F32 (checked by the entry point).
+// branch_dtype is BF16, FP16 or FP32 (checked by the entry point), read as is.
 template <int XDT>
-int gate_by_branch(int pdt, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
-  if constexpr (XDT != M5K_F32) {
-    if (branch_dtype == M5K_F32) return gate_by_param<XDT, M5K_F32>(pdt, p, rows, st);
+int gate_by_branch(bool bf16_gate, int branch_dtype, const PrepParams& p, int64_t rows, hipStream_t st) {
+  switch (branch_dtype) {
+    case M5K_BF16: return gate_by_param<XDT, M5K_BF16>(bf16_gate, p, rows, st);
+    case M5K_F16: return gate_by_param<XDT, M5K_F16>(bf16_gate, p, rows, st);
+    default: return gate_by_param<XDT, M5K_F32>(bf16_gate, p, rows, st);
   }
-  return gate_by_param<XDT, XDT>(pdt, p, rows, st);
 }
 
 bool a16(const void* ptr) { return ptr == nullptr || aligned16(ptr); }
@@ -519,14 +527,34 @@ float exact_inv_k(int64_t k) {
   return (k & (k - 1)) == 0 ? std::ldexp(1.0f, -__builtin_ctzll(static_cast<unsigned long long>(k))) : 0.0f;
 }
 
-int check_common(const void* x, int x_dtype, int64_t rows, int64_t k, int param_dtype, const char* name) {
+bool float_code(int dt) { return dt == M5K_BF16 || dt == M5K_F16 || dt == M5K_F32; }
+
+// The tables' dtypes from a param_dtype argument: one float code for every table, or
+// M5K_PARAM_TABLES(gamma, scale, shift, gate).  all_bf16 selects the compile-time BF16 kernels.
+int unpack_param_dtypes(int param_dtype, PrepParams& p, bool& all_bf16, const char* name) {
+  if (float_code(param_dtype)) {
+    p.dt_gamma = p.dt_scale = p.dt_shift = p.dt_gate = param_dtype;
+  } else {
+    M5K_REQUIRE((param_dtype & ~0x1FF) == 0 && (param_dtype & M5K_PARAM_PER_TABLE) != 0,
+                "%s: parameter dtype %d is neither a float dtype code nor M5K_PARAM_TABLES(...)", name, param_dtype);
+    p.dt_gamma = param_dtype & 3;
+    p.dt_scale = (param_dtype >> 2) & 3;
+    p.dt_shift = (param_dtype >> 4) & 3;
+    p.dt_gate = (param_dtype >> 6) & 3;
+    M5K_REQUIRE(float_code(p.dt_gamma) && float_code(p.dt_scale) && float_code(p.dt_shift) && float_code(p.dt_gate),
+                "%s: M5K_PARAM_TABLES fields must be float dtype codes (got 0x%x)", name, param_dtype);
+  }
+  all_bf16 = p.dt_gamma == M5K_BF16 && p.dt_scale == M5K_BF16 && p.dt_shift == M5K_BF16 && p.dt_gate == M5K_BF16;
+  return M5K_OK;
+}
+
+int check_common(const void* x, int x_dtype, int64_t rows, int64_t k, const char* name) {
   M5K_REQUIRE(x, "%s: null input", name);
   M5K_REQUIRE(rows > 0 && k > 0 && rows <= 0x7FFFFFFF, "%s: bad shape [%lld,%lld]", name, (long long)rows,
               (long long)k);
   M5K_REQUIRE(k % 8 == 0, "%s: K=%lld must be a multiple of 8", name, (long long)k);
   M5K_REQUIRE(x_dtype == M5K_BF16 || x_dtype == M5K_F16 || x_dtype == M5K_F32, "%s: unsupported input dtype %d",
               name, x_dtype);
-  M5K_REQUIRE(param_dtype == M5K_BF16 || param_dtype == M5K_F32, "%s: parameter dtype must be BF16 or F32", name);
   return M5K_OK;
 }
 
@@ -546,24 +574,27 @@ extern "C" int m5k_norm_hadamard_quantize(const void* x, int x_dtype, int64_t ro
                                           void* residual_out, void* stream) {
   clear_error();
   const char* name = "m5k_norm_hadamard_quantize";
-  if (int rc = check_common(x, x_dtype, rows, k, param_dtype, name)) return rc;
+  if (int rc = check_common(x, x_dtype, rows, k, name)) return rc;
   M5K_REQUIRE(gamma && scale && shift && signs && q && scales, "%s: null pointer", name);
   M5K_REQUIRE(block >= 32 && block <= 1024 && (block & (block - 1)) == 0 && k % block == 0,
               "%s: block %d must be a power of two in [32,1024] dividing K", name, block);
   M5K_REQUIRE(!branch || (gate && residual_out), "%s: gated prep needs gate and residual_out", name);
-  M5K_REQUIRE(!branch || branch_dtype == x_dtype || branch_dtype == M5K_F32,
-              "%s: branch dtype %d must be the input dtype or F32", name, branch_dtype);
+  M5K_REQUIRE(!branch || float_code(branch_dtype), "%s: branch dtype %d must be BF16, F16 or F32", name,
+              branch_dtype);
   M5K_REQUIRE(epsilon > 0.0f, "%s: epsilon must be positive", name);
   M5K_REQUIRE(a16(x) && a16(branch) && a16(gate) && a16(gamma) && a16(scale) && a16(shift) && a16(residual_out) &&
                   (reinterpret_cast<uintptr_t>(signs) & 7u) == 0 && (reinterpret_cast<uintptr_t>(q) & 7u) == 0,
               "%s: misaligned buffers", name);
   PrepParams p{x,     branch, gate, gate_row_map, gamma,  scale, shift, row_map, signs, q, scales, residual_out,
                nullptr, k, epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0, exact_inv_k(k)};
+  bool all_bf16 = false;
+  if (int rc = unpack_param_dtypes(param_dtype, p, all_bf16, name)) return rc;
+  if (!branch) all_bf16 = p.dt_gamma == M5K_BF16 && p.dt_scale == M5K_BF16 && p.dt_shift == M5K_BF16;
   hipStream_t st = as_stream(stream);
   switch (x_dtype) {
-    case M5K_BF16: return fused_by_param<M5K_BF16>(param_dtype, block, branch_dtype, p, rows, st);
-    case M5K_F16: return fused_by_param<M5K_F16>(param_dtype, block, branch_dtype, p, rows, st);
-    default: return fused_by_param<M5K_F32>(param_dtype, block, branch_dtype, p, rows, st);
+    case M5K_BF16: return fused_by_param<M5K_BF16>(all_bf16, block, branch_dtype, p, rows, st);
+    case M5K_F16: return fused_by_param<M5K_F16>(all_bf16, block, branch_dtype, p, rows, st);
+    default: return fused_by_param<M5K_F32>(all_bf16, block, branch_dtype, p, rows, st);
   }
 }
 
@@ -572,17 +603,20 @@ extern "C" int m5k_norm_modulate(const void* x, int x_dtype, int64_t rows, int64
                                  int norm, float epsilon, int round_to_input, void* y, void* stream) {
   clear_error();
   const char* name = "m5k_norm_modulate";
-  if (int rc = check_common(x, x_dtype, rows, k, param_dtype, name)) return rc;
+  if (int rc = check_common(x, x_dtype, rows, k, name)) return rc;
   M5K_REQUIRE(gamma && scale && shift && y, "%s: null pointer", name);
   M5K_REQUIRE(epsilon > 0.0f, "%s: epsilon must be positive", name);
   M5K_REQUIRE(a16(x) && a16(gamma) && a16(scale) && a16(shift) && a16(y), "%s: misaligned buffers", name);
   PrepParams p{x, nullptr, nullptr, nullptr, gamma,   scale, shift, row_map, nullptr, nullptr, nullptr, nullptr,
                y, k,       epsilon, norm == M5K_NORM_LAYER ? 1 : 0, round_to_input ? 1 : 0, exact_inv_k(k)};
+  bool all_bf16 = false;
+  if (int rc = unpack_param_dtypes(param_dtype, p, all_bf16, name)) return rc;
+  all_bf16 = p.dt_gamma == M5K_BF16 && p.dt_scale == M5K_BF16 && p.dt_shift == M5K_BF16;  // no gate here
   hipStream_t st = as_stream(stream);
   switch (x_dtype) {
-    case M5K_BF16: return norm_by_param<M5K_BF16>(param_dtype, p, rows, st);
-    case M5K_F16: return norm_by_param<M5K_F16>(param_dtype, p, rows, st);
-    default: return norm_by_param<M5K_F32>(param_dtype, p, rows, st);
+    case M5K_BF16: return norm_by_param<M5K_BF16>(all_bf16, p, rows, st);
+    case M5K_F16: return norm_by_param<M5K_F16>(all_bf16, p, rows, st);
+    default: return norm_by_param<M5K_F32>(all_bf16, p, rows, st);
   }
 }
 
@@ -591,17 +625,19 @@ extern "C" int m5k_gated_residual_add(const void* residual, int dtype, int64_t r
                                       const int32_t* gate_row_map, void* out, void* stream) {
   clear_error();
   const char* name = "m5k_gated_residual_add";
-  if (int rc = check_common(residual, dtype, rows, k, gate_dtype, name)) return rc;
+  if (int rc = check_common(residual, dtype, rows, k, name)) return rc;
   M5K_REQUIRE(branch && gate && out, "%s: null pointer", name);
-  M5K_REQUIRE(branch_dtype == dtype || branch_dtype == M5K_F32, "%s: branch dtype %d must be the residual dtype or F32",
-              name, branch_dtype);
+  M5K_REQUIRE(float_code(branch_dtype), "%s: branch dtype %d must be BF16, F16 or F32", name, branch_dtype);
+  M5K_REQUIRE(float_code(gate_dtype), "%s: gate dtype %d must be BF16, F16 or F32", name, gate_dtype);
   M5K_REQUIRE(a16(residual) && a16(branch) && a16(gate) && a16(out), "%s: misaligned buffers", name);
   PrepParams p{residual, branch, gate, gate_row_map, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                out,      nullptr, k,   1.0f,         0,       0};
+  p.dt_gamma = p.dt_scale = p.dt_shift = p.dt_gate = gate_dtype;
   hipStream_t st = as_stream(stream);
+  const bool bf16_gate = gate_dtype == M5K_BF16;
   switch (dtype) {
-    case M5K_BF16: return gate_by_branch<M5K_BF16>(gate_dtype, branch_dtype, p, rows, st);
-    case M5K_F16: return gate_by_branch<M5K_F16>(gate_dtype, branch_dtype, p, rows, st);
-    default: return gate_by_branch<M5K_F32>(gate_dtype, branch_dtype, p, rows, st);
+    case M5K_BF16: return gate_by_branch<M5K_BF16>(bf16_gate, branch_dtype, p, rows, st);
+    case M5K_F16: return gate_by_branch<M5K_F16>(bf16_gate, branch_dtype, p, rows, st);
+    default: return gate_by_branch<M5K_F32>(bf16_gate, branch_dtype, p, rows, st);
   }
 }

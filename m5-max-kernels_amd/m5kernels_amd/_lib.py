@@ -17,6 +17,12 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libm5k.so"
 F32, F16, BF16, I8, U8, I32 = 0, 1, 2, 3, 4, 5
 QUANT_INT8, QUANT_FP8 = 0, 1
 NORM_RMS, NORM_LAYER = 0, 1
+PARAM_PER_TABLE = 0x100  # include/m5k.h M5K_PARAM_PER_TABLE
+
+
+def param_tables(gamma: int, scale: int, shift: int, gate: int = BF16) -> int:
+    """M5K_PARAM_TABLES(gamma, scale, shift, gate): one float dtype code per prep table."""
+    return PARAM_PER_TABLE | gamma | (scale << 2) | (shift << 4) | (gate << 6)
 
 _DTYPE_CODES = {
     torch.float32: F32,

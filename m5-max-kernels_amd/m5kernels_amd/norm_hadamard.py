@@ -12,11 +12,9 @@ Platform notes (contract unchanged):
 
 * ``threads`` (128/256), ``passes`` ("one_read"/"two_read") and ``tag`` are validated as in
   the reference; the gfx950 kernel always keeps the row in registers with 256 lanes.
-* gamma/scale/shift/gate are consumed as FP32 (bf16 tables are read natively; fp16 tables
-  are widened to FP32 first, exactly).
-* A ``branch`` of another float dtype than the residual is widened to FP32 (exact for
-  BF16/FP16) and read as FP32 by the kernel: ``float(branch)`` is the same value, so the
-  FP32 product-then-add and the single residual-dtype cast are unchanged.
+* gamma/scale/shift/gate and ``branch`` are read in their own float dtypes by the one kernel
+  (no host-side casts): every table may have its own dtype, and the branch's need not be the
+  residual's.  Each value enters the FP32 arithmetic exactly, as ``float(...)`` does.
 * K must be a multiple of 8 (always true with a Hadamard block; checked for unfused_norm
   and gated_residual_add).
 """
@@ -105,26 +103,23 @@ def _validate_gate(residual, branch, gate, gate_row_map):
             raise ValueError("gate_row_map must be an int32 vector of length M")
 
 
-def _params(*tensors):
-    """Parameter tables in one dtype the kernels read natively: bf16 if all are bf16, else FP32."""
-    present = [t for t in tensors if t is not None]
-    if all(t.dtype == torch.bfloat16 for t in present):
-        code = _lib.BF16
-        out = [None if t is None else _lib.aligned_device_tensor(t, "parameter") for t in tensors]
-    else:
-        code = _lib.F32
-        out = [None if t is None else _lib.aligned_device_tensor(t.to(torch.float32), "parameter") for t in tensors]
-    return code, out
+def _params(gamma, scale, shift, gate=None):
+    """The device tables as given and their param_dtype code: BF16 when every table is BF16, else
+    one dtype code per table (M5K_PARAM_TABLES; an absent gate's field is unused)."""
+    tables = (gamma, scale, shift, gate)
+    out = [None if t is None else _lib.aligned_device_tensor(t, "parameter") for t in tables]
+    codes = [_lib.BF16 if t is None else _lib.dtype_code(t) for t in out]
+    if all(c == _lib.BF16 for c in codes):
+        return _lib.BF16, out
+    return _lib.param_tables(*codes), out
 
 
 def _map(t, name):
     return None if t is None else _lib.device_tensor(t, name)
 
 
-def _branch(branch, residual):
-    """Device branch and its dtype code: the residual's dtype, else exactly widened to FP32."""
-    if branch.dtype != residual.dtype:
-        branch = branch.to(torch.float32)
+def _branch(branch):
+    """Device branch and its dtype code (any float dtype; the kernels read it as is)."""
     branch = _lib.aligned_device_tensor(branch, "branch")
     return branch, _lib.dtype_code(branch)
 
@@ -143,7 +138,7 @@ def _prep(x, gamma, scale, shift, signs, block_size, norm, epsilon, round_output
     s = torch.empty((rows,), dtype=torch.float32, device=x.device)
     r_next, branch_code = None, _lib.dtype_code(x)
     if branch is not None:
-        branch, branch_code = _branch(branch, x)
+        branch, branch_code = _branch(branch)
         r_next = torch.empty_like(x)
     _lib.call(
         "m5k_norm_hadamard_quantize",
@@ -223,13 +218,14 @@ def gated_residual_add(residual, branch, gate, *, gate_row_map=None, threads=256
     if residual.shape[1] % 8:
         raise NotImplementedError("K must be a multiple of 8 on MI355X")
     residual = _lib.aligned_device_tensor(residual, "residual")
-    branch, branch_code = _branch(branch, residual)
-    pdt, (gate_d,) = _params(gate)
+    branch, branch_code = _branch(branch)
+    gate_d = _lib.aligned_device_tensor(gate, "gate")
     out = torch.empty_like(residual)
     rows, k = residual.shape
     _lib.call(
         "m5k_gated_residual_add",
-        _lib.ptr(residual), _lib.dtype_code(residual), rows, k, _lib.ptr(branch), branch_code, _lib.ptr(gate_d), pdt,
+        _lib.ptr(residual), _lib.dtype_code(residual), rows, k, _lib.ptr(branch), branch_code, _lib.ptr(gate_d),
+        _lib.dtype_code(gate_d),
         _lib.ptr(_map(gate_row_map, "gate_row_map")), _lib.ptr(out), _lib.stream_of(residual),
     )
     return out
@@ -252,7 +248,7 @@ def unfused_norm(
     if x.shape[1] % 8:
         raise NotImplementedError("K must be a multiple of 8 on MI355X")
     x = _lib.aligned_device_tensor(x, "x")
-    pdt, (gamma_d, scale_d, shift_d) = _params(gamma, scale, shift)
+    pdt, (gamma_d, scale_d, shift_d, _) = _params(gamma, scale, shift)
     out_dtype = x.dtype if round_output == "input" else torch.float32
     y = torch.empty(tuple(x.shape), dtype=out_dtype, device=x.device)
     rows, k = x.shape

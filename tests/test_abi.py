@@ -67,3 +67,23 @@ def test_product_path_never_imports_the_oracle():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.load(tmp_path / "libm5k.so")
+
+
+def test_prep_param_dtype_codes():
+    """M5K_PARAM_TABLES as the header defines it, and the prep entry points' checks of it (they
+    fail before any launch: the pointers below are never dereferenced)."""
+    text = HEADER.read_text()
+    assert int(re.search(r"#define M5K_PARAM_PER_TABLE (0x[0-9a-fA-F]+)", text).group(1), 16) == _lib.PARAM_PER_TABLE
+    assert "((gamma) | ((scale) << 2) | ((shift) << 4) | ((gate) << 6))" in text.replace("M5K_PARAM_PER_TABLE | ", "(")
+    assert _lib.param_tables(_lib.F16, _lib.F32, _lib.BF16, _lib.F16) == 0x100 | 1 | (0 << 2) | (2 << 4) | (1 << 6)
+    lib = _lib.load()
+    fake = ctypes.c_void_p(64)
+    args = lambda pdt: (fake, _lib.BF16, 2, 256, None, _lib.BF16, None, None, fake, fake, fake, pdt, None, fake,  # noqa: E731
+                        128, _lib.NORM_RMS, ctypes.c_float(1e-5), 1, fake, fake, None, None)
+    assert lib.m5k_norm_hadamard_quantize(*args(7)) == 1
+    assert b"neither a float dtype code" in lib.m5k_last_error()
+    assert lib.m5k_norm_hadamard_quantize(*args(_lib.PARAM_PER_TABLE | 3)) == 1
+    assert b"M5K_PARAM_TABLES fields" in lib.m5k_last_error()
+    assert lib.m5k_norm_modulate(fake, _lib.BF16, 2, 256, fake, fake, fake, 0x2FF, None, _lib.NORM_RMS,
+                                 ctypes.c_float(1e-5), 1, fake, None) == 1
+    assert b"neither a float dtype code" in lib.m5k_last_error()

@@ -324,6 +324,61 @@ def test_gated_prep_mixed_branch_dtype_bit_exact(norm, dtype, branch_dtype, mapp
 
 
 @pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("tables", [("fp16", "fp32", "bf16", "fp16"), ("fp32", "fp32", "fp32", "fp32"),
+                                    ("fp16", "fp16", "fp16", "fp16"), ("bf16", "bf16", "fp32", "bf16"),
+                                    ("bf16", "fp16", "bf16", "fp32")])
+@pytest.mark.parametrize("dtype,branch_dtype,width", [("bf16", "fp16", 4096), ("fp16", "fp32", 5376),
+                                                      ("fp32", "bf16", 4096), ("bf16", "bf16", 4096)])
+def test_prep_mixed_table_dtypes_one_dispatch_bit_exact(norm, tables, dtype, branch_dtype, width, device,
+                                                        monkeypatch):
+    """gamma, scale, shift and gate each in their own float dtype, and a branch in any float dtype:
+    the one prep dispatch reads every input as given (the reference's kernel reads float() of each
+    input in its own dtype, norm_hadamard.py:67-70), so no host-side cast runs.  R_next, codes and
+    scales equal the fixed-order oracle fed the same values, the ungated prep and the staged
+    comparators agree, and the pointers handed to the C ABI are the caller's own tensors."""
+    from m5kernels_amd import _lib
+
+    rng = np.random.default_rng(733)
+    shape = (6, width)
+    rt = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(device).to(DT[dtype])
+    bt = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * 2).to(device).to(DT[branch_dtype])
+    g_dt, sc_dt, sh_dt, gt_dt = (DT[t] for t in tables)
+    gamma = torch.from_numpy(1 + 0.1 * rng.standard_normal(width).astype(np.float32)).to(device).to(g_dt)
+    scale = torch.from_numpy(0.1 * rng.standard_normal((2, width)).astype(np.float32)).to(device).to(sc_dt)
+    shift = torch.from_numpy(0.1 * rng.standard_normal((2, width)).astype(np.float32)).to(device).to(sh_dt)
+    gate = torch.from_numpy(rng.uniform(-0.8, 0.8, size=(3, width)).astype(np.float32)).to(device).to(gt_dt)
+    row_map = torch.tensor([1, 0, 0, 1, 1, 0], dtype=torch.int32, device=device)
+    gmap = torch.tensor([2, 0, 1, 1, 2, 0], dtype=torch.int32, device=device)
+    signs = torch.from_numpy(ref.hadamard_signs(width, 31)).to(device)
+    calls = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        calls.append((name, args))
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    q, s, upd = fused_gated_residual_norm_hadamard_quantize(rt, bt, gate, gamma, scale, shift, signs, 256, norm=norm,
+                                                            gate_row_map=gmap, row_map=row_map)
+    name, args = calls[-1]
+    assert name == "m5k_norm_hadamard_quantize"
+    handed = {args[i].value for i in (0, 4, 6, 8, 9, 10)}
+    assert handed == {t.data_ptr() for t in (rt, bt, gate, gamma, scale, shift)}
+    assert args[5] == _lib.dtype_code(bt)
+    oq, os_, orn = _oracle_prep(rt, gamma, scale, shift, signs, 256, norm=norm, branch=bt, gate=gate,
+                                gate_row_map=gmap, row_map=row_map)
+    np.testing.assert_array_equal(upd.float().cpu().numpy(), orn)
+    np.testing.assert_array_equal(np_of(q), oq)
+    np.testing.assert_array_equal(np_of(s), os_)
+    assert torch.equal(gated_residual_add(rt, bt, gate, gate_row_map=gmap), upd)
+    q2, s2 = fused_norm_hadamard_quantize(upd, gamma, scale, shift, signs, 256, norm=norm, row_map=row_map)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    f32 = lambda t: t.float()  # noqa: E731  (exact widening: the same values in FP32 tables)
+    y = unfused_norm(upd, gamma, scale, shift, norm=norm, row_map=row_map)
+    assert torch.equal(y, unfused_norm(upd, f32(gamma), f32(scale), f32(shift), norm=norm, row_map=row_map))
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
 @pytest.mark.parametrize("gated", [False, True])
 @pytest.mark.parametrize("dtype,block,width,round_output", [("bf16", 128, 4096, "input"), ("fp32", 32, 768, "input"),
                                                             ("bf16", 1024, 4096, "fp32"), ("fp16", 64, 2048, "input"),
@@ -380,5 +435,8 @@ def test_gated_residual_add_mixed_dtype_through_c_abi(device):
                                     .astype(np.float32))
     np.testing.assert_array_equal(bits_of(out), expected)
     with pytest.raises(RuntimeError, match="branch dtype"):
-        _lib.call("m5k_gated_residual_add", _lib.ptr(res), _lib.BF16, 3, 256, _lib.ptr(branch), _lib.F16,
+        _lib.call("m5k_gated_residual_add", _lib.ptr(res), _lib.BF16, 3, 256, _lib.ptr(branch), _lib.I8,
                   _lib.ptr(gate), _lib.F32, None, _lib.ptr(out), _lib.stream_of(res))
+    with pytest.raises(RuntimeError, match="gate dtype"):
+        _lib.call("m5k_gated_residual_add", _lib.ptr(res), _lib.BF16, 3, 256, _lib.ptr(branch), _lib.F32,
+                  _lib.ptr(gate), _lib.I32, None, _lib.ptr(out), _lib.stream_of(res))
