@@ -858,7 +858,8 @@ def ceiling_kernels(torch, dev, aq, wq):
     """name -> launcher of the MFMA ceiling kernels (libm5k_diag.so) on the FFN-down codes: the
     GEMM main loop's v_mfma_i32_16x16x64_i8 stream alone, register-resident fragments read from
     the bench's own A and W codes, K / 128 iterations = the GEMM's MFMA count; the same on
-    constant codes (all 1); and the v_mfma_i32_32x32x32_i8 form of the same work."""
+    constant codes (all 1); the v_mfma_i32_32x32x32_i8 form of the same work; and the 16 x 16 x 64
+    stream on four waves (one per SIMD) instead of eight."""
     import ctypes
 
     lib = _diag_lib()
@@ -874,7 +875,7 @@ def ceiling_kernels(torch, dev, aq, wq):
         return run
 
     return {"mfma_ceiling_16x16x64": launcher(16, 0), "mfma_ceiling_16x16x64_constant": launcher(16, 1),
-            "mfma_ceiling_32x32x32": launcher(32, 0)}
+            "mfma_ceiling_32x32x32": launcher(32, 0), "mfma_ceiling_16x16x64_one_wave_per_simd": launcher(4, 0)}
 
 
 def mfma_ceiling(torch, dev, rounds=8, reps=10):

@@ -607,10 +607,27 @@ struct AccGeom {
   __device__ __forceinline__ int col(int j) const { return c0 + j * MD; }
 };
 
-// Row and column scales of a tile, staged in the LDS after the 16-bit tile by one coalesced
-// load per thread (0 past the matrix; every thread of the workgroup calls it after the main
-// loop, whose last barrier freed the LDS).  Lanes then read their scales from the LDS one
-// block row at a time, so the epilogue waits for HBM once and holds few extra registers.
+// A tile's row and column scales, one per thread (threads [0, BM) the rows, [BM, BM + TN) the
+// columns; 0 past the matrix), loaded before the main loop so that their latency hides behind it
+// instead of opening the epilogue: 0.1-0.7 us less per tile round (A/B, same bits: 4096^3
+// 56.1 -> 55.4 us, FFN-up 211.0 -> 209.1 us).  The load is issued before the loop's first DMA,
+// so the loop's in-order vmcnt waits cover it and their counts stay exact.
+template <class G>
+struct TileScalePrefetch {
+  static_assert(G::THREADS >= BM + G::TN, "one scale per thread");
+  float v;
+  __device__ __forceinline__ TileScalePrefetch(const float* __restrict__ sa, const float* __restrict__ sb, int M,
+                                               int N, int m0, int n0) {
+    const int t = threadIdx.x;
+    const int m = m0 + t, n = n0 + t - BM;
+    v = t < BM ? (m < M ? sa[m] : 0.0f) : (t < BM + G::TN && n < N ? sb[n] : 0.0f);
+  }
+};
+
+// Row and column scales of a tile, staged in the LDS after the 16-bit tile (every thread of the
+// workgroup constructs it after the main loop, whose last barrier freed the LDS): from global
+// memory, one coalesced load per thread, or from the prefetched values.  Lanes then read their
+// scales from the LDS one block row at a time, so the epilogue holds few extra registers.
 template <class G>
 struct TileScales {
   const float* s;  // rows [0, BM), then columns [BM, BM + G::TN)
@@ -621,6 +638,12 @@ struct TileScales {
       const int m = m0 + t, n = n0 + t - BM;
       w[t] = t < BM ? (m < M ? sa[m] : 0.0f) : (n < N ? sb[n] : 0.0f);
     }
+    __syncthreads();
+    s = w;
+  }
+  __device__ __forceinline__ TileScales(const TileScalePrefetch<G>& pre, int tid) {
+    float* w = reinterpret_cast<float*>(g_lds + EPI_SCALES_OFFSET);
+    if (tid < BM + G::TN) w[tid] = pre.v;
     __syncthreads();
     s = w;
   }

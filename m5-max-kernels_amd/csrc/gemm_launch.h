@@ -37,6 +37,14 @@ struct EpiParams {
 // Wave grid used by every GEMM kernel of the library.
 using KernelGrid = Grid8;
 
+// The tile's scales ahead of the main loop (quantized modes with a scale epilogue; nothing for the
+// others).
+template <int MODE, bool RAW, class G>
+__device__ __forceinline__ TileScalePrefetch<G> prefetch_scales(const EpiParams& p, int M, int N, int m0, int n0) {
+  if constexpr ((MODE == I8 || MODE == F8) && !RAW) return TileScalePrefetch<G>(p.sa, p.sb, M, N, m0, n0);
+  else return TileScalePrefetch<G>(nullptr, nullptr, 0, 0, 0, 0);
+}
+
 // Scale epilogue of one 256 x G::TN tile (every thread of the workgroup calls it; the LDS is
 // free).  RAW writes the INT32 accumulators.  The per-row and per-column operands of the
 // lane's elements (scales, bias vector) are loaded in one batch before the arithmetic, and a
@@ -44,7 +52,7 @@ using KernelGrid = Grid8;
 // few times instead of once per element.
 template <int MODE, int OUT_DT, int BIAS, int GATE, bool RAW, class G = KernelGrid>
 __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int N, int m0, int n0,
-                                         const EpiParams& p) {
+                                         const EpiParams& p, const TileScalePrefetch<G>& pre) {
   using Geo = AccGeom<MODE, G>;
   constexpr bool QUANT = MODE == I8 || MODE == F8;
   const int tid = tid_after_mainloop();
@@ -64,7 +72,7 @@ __device__ __forceinline__ void epilogue(const AccTile<MODE, G>& acc, int M, int
     float cs[QUANT ? Geo::FN : 1];
     const float* sc = nullptr;
     if constexpr (QUANT) {
-      const TileScales<G> ts(p.sa, p.sb, M, N, m0, n0, tid);
+      const TileScales<G> ts(pre, tid);
       sc = ts.s;
 #pragma unroll
       for (int j = 0; j < Geo::FN; ++j) cs[j] = ts.col(geo.col(j));
@@ -211,10 +219,11 @@ __global__ __launch_bounds__(G::THREADS, 1) void gemm_kernel(const uint8_t* __re
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * G::TN;
+  const TileScalePrefetch<G> pre = prefetch_scales<MODE, RAW, G>(p, M, N, m0, n0);
   AccTile<MODE, G> acc;
   if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
-  epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
+  epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p, pre);
 }
 
 // ---- Mixed tiles for a partial last round ---------------------------------------------------
@@ -244,9 +253,10 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_mixed_kernel(cons
     int tm, tn;
     band_coords(xcd_logical(bid, full), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    const TileScalePrefetch<G> pre = prefetch_scales<MODE, RAW, G>(p, M, N, m0, n0);
     AccTile<MODE, G> acc;
     mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
-    epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
+    epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p, pre);
   } else {
     using G = HalfGrid;
     const int h = xcd_logical(bid - full, 2 * (tiles_m * tiles_n - full));
@@ -254,9 +264,10 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void gemm_mixed_kernel(cons
     band_coords(full + (h >> 1), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN + (h & 1) * G::TN;
     if (n0 >= N) return;  // right half of a last tile column at most 128 wide (whole workgroup)
+    const TileScalePrefetch<G> pre = prefetch_scales<MODE, RAW, G>(p, M, N, m0, n0);
     AccTile<MODE, G> acc;
     mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
-    epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p);
+    epilogue<MODE, OUT_DT, BIAS, GATE, RAW, G>(acc, M, N, m0, n0, p, pre);
   }
 }
 

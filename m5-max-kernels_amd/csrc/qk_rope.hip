@@ -235,8 +235,7 @@ __device__ __forceinline__ uint4 norm_rope_fast(const float (&z)[8], const LaneR
 // released, then 16-lane groups normalize and rotate (row, head) pairs.
 template <int MODE, class G>
 __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, int M, int N, int m0, int n0,
-                                                 const float* __restrict__ sa, const float* __restrict__ sb,
-                                                 const QkParams& p, int fast) {
+                                                 const TileScalePrefetch<G>& pre, const QkParams& p, int fast) {
   static_assert(G::TN % HEAD == 0, "projection tiles hold whole heads");
   constexpr int HPT = G::TN / HEAD;  // heads per tile
   // Everything the epilogue loads depends on the lane index taken here, after the main loop,
@@ -258,7 +257,7 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
     float cs[Geo::FN];
     const float* sc = nullptr;
     if constexpr (MODE == I8) {
-      const TileScales<G> ts(sa, sb, M, N, m0, n0, tid_after);
+      const TileScales<G> ts(pre, tid_after);
       sc = ts.s;
 #pragma unroll
       for (int j = 0; j < Geo::FN; ++j) cs[j] = ts.col(geo.col(j));
@@ -368,6 +367,15 @@ __device__ __forceinline__ void qk_tile_epilogue(const AccTile<MODE, G>& acc, in
   }
 }
 
+// The INT8 tile's scales ahead of the main loop (the BF16 projection has none).
+template <int MODE, class G>
+__device__ __forceinline__ TileScalePrefetch<G> qk_prefetch_scales(const float* __restrict__ sa,
+                                                                   const float* __restrict__ sb, int M, int N, int m0,
+                                                                   int n0) {
+  if constexpr (MODE == I8) return TileScalePrefetch<G>(sa, sb, M, N, m0, n0);
+  else return TileScalePrefetch<G>(nullptr, nullptr, 0, 0, 0, 0);
+}
+
 template <int MODE, bool ALIGNED>
 __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const uint8_t* __restrict__ A,
                                                                           const uint8_t* __restrict__ B, int M, int N,
@@ -379,10 +387,11 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_fused_kernel(const 
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  const TileScalePrefetch<G> pre = qk_prefetch_scales<MODE, G>(sa, sb, M, N, m0, n0);
   AccTile<MODE, G> acc;
   if constexpr (ALIGNED) mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
   else mainloop_staged<MODE, G>(A, B, M, N, Kb, m0, n0, acc);
-  qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, sa, sb, p, fast);
+  qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, pre, p, fast);
 }
 
 // The mixed schedule of the GEMM library (gemm_mixed_kernel) for the fused projection: the
@@ -404,9 +413,10 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_mixed_kernel(const 
     int tm, tn;
     band_coords(xcd_logical(bid, full), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    const TileScalePrefetch<G> pre = qk_prefetch_scales<MODE, G>(sa, sb, M, N, m0, n0);
     AccTile<MODE, G> acc;
     mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
-    qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, sa, sb, p, fast);
+    qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, pre, p, fast);
   } else {
     using G = gemm::detail::HalfGrid;
     const int h = xcd_logical(bid - full, 2 * (tiles_m * tiles_n - full));
@@ -414,9 +424,10 @@ __global__ __launch_bounds__(KernelGrid::THREADS, 1) void qk_mixed_kernel(const 
     band_coords(full + (h >> 1), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN + (h & 1) * G::TN;
     if (n0 >= N) return;  // right half of a last tile column one head wide (whole workgroup)
+    const TileScalePrefetch<G> pre = qk_prefetch_scales<MODE, G>(sa, sb, M, N, m0, n0);
     AccTile<MODE, G> acc;
     mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, 0, k_stages(Kb));
-    qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, sa, sb, p, fast);
+    qk_tile_epilogue<MODE, G>(acc, M, N, m0, n0, pre, p, fast);
   }
 }
 

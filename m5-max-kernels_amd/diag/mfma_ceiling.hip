@@ -8,7 +8,9 @@
 // v_mfma_i32_16x16x64_i8 (or 2 x 2 x 4 x 2 x 2 v_mfma_i32_32x32x32_i8 of the same K bytes) back to
 // back.  With iters = K / 128 it performs the GEMM's MFMA count on data with the GEMM's value
 // distribution, so its duration bounds what the matrix cores deliver at the clock the chip holds
-// on that data.  `constant` replaces every code with 1 (the low-power case).
+// on that data.  `constant` replaces every code with 1 (the low-power case).  The one-wave form
+// (md = 4) runs the same MFMA stream as 4 waves, one per SIMD, each doing the work of two: it
+// measures what a single wave's back-to-back 16 x 16 x 64 MFMAs can issue.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -19,8 +21,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-template <int MD>
-__global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const int8_t* __restrict__ A,
+template <int MD, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 1) void mfma_ceiling_kernel(const int8_t* __restrict__ A,
                                                               const int8_t* __restrict__ B, int tiles_n,
                                                               int64_t kb, int iters, int constant,
                                                               int32_t* __restrict__ out) {
@@ -29,7 +31,7 @@ __global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const int8_t* __re
   constexpr int KPER = MD == 16 ? 64 : 32;  // K bytes of one MFMA
   constexpr int SLICES = 128 / KPER;        // the K bytes of one 128-byte GEMM stage
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / 4, wn = wave % 4;
+  const int wm = (wave % 8) / 4, wn = wave % 4;
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
   const int r_in = lane % MD, chunk = lane / MD;
   v4i a[SLICES][FM], b[SLICES][FN];
@@ -56,7 +58,7 @@ __global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const int8_t* __re
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
-  for (int it = 0; it < iters; ++it) {
+  for (int it = 0; it < iters * (8 / WAVES); ++it) {
 #pragma unroll
     for (int s = 0; s < SLICES; ++s)
 #pragma unroll
@@ -82,17 +84,18 @@ __global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const int8_t* __re
 }  // namespace
 
 // m, n multiples of 256; kb >= 128 a multiple of 16; out holds (m / 256) * (n / 256) * 512 int32.
-// md: 16 (v_mfma_i32_16x16x64_i8) or 32 (v_mfma_i32_32x32x32_i8).  Returns 0 or a HIP error code
-// (1 for invalid arguments).
+// md: 16 (v_mfma_i32_16x16x64_i8), 32 (v_mfma_i32_32x32x32_i8) or 4 (16 x 16 x 64 on one wave per
+// SIMD).  Returns 0 or a HIP error code (1 for invalid arguments).
 extern "C" int m5k_diag_mfma_ceiling(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int64_t kb, int iters,
                                      int constant, int md, int32_t* out, void* stream) {
   if (!a || !b || !out || m <= 0 || n <= 0 || m % 256 || n % 256 || kb < 128 || kb % 16 || iters < 0 ||
-      (md != 16 && md != 32) || (m / 256) * (n / 256) > 0x7FFFFFFF)
+      (md != 16 && md != 32 && md != 4) || (m / 256) * (n / 256) > 0x7FFFFFFF)
     return 1;
   const int tiles_n = static_cast<int>(n / 256);
   const dim3 grid(static_cast<unsigned>((m / 256) * tiles_n)), block(512);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (md == 16) mfma_ceiling_kernel<16><<<grid, block, 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
-  else mfma_ceiling_kernel<32><<<grid, block, 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
+  if (md == 16) mfma_ceiling_kernel<16, 8><<<grid, block, 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
+  else if (md == 32) mfma_ceiling_kernel<32, 8><<<grid, block, 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
+  else mfma_ceiling_kernel<16, 4><<<grid, dim3(256), 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
   return static_cast<int>(hipGetLastError());
 }
