@@ -13,11 +13,11 @@ baseline (the oracle's C/OpenMP W8A8 on a bounded row sample, rank 0 only).
 Timing.  After the W warmup steps, further untimed steps run until at least --settle-seconds
 (0.4 s) of device time has passed, whatever W is: on MI355X the first ~100 steps after idle run
 10-15% slower while the clocks ramp (the count is reported as settle_steps).  The headline region has
-only a start and an end event around the K steps (per-step timing events add ~3%); a second
-pass of K steps gives the per-kernel durations that the roofline uses: each kernel records its
-own start and end into a pair of events (m5k_time_next_launch).  Events recorded between the
-kernels would add their own packets, and default ones would write back and invalidate the caches
-between the quantizer and the GEMM, which changes both.
+only a start and an end event around the K steps (per-step timing events add ~3%).  The
+per-kernel durations that the roofline uses come from passes with no event between two kernels
+(an event there, even one without a system fence, slows both kernels it separates): K GEMM
+launches back to back between one event pair, and K quantizer launches cycling over activation
+sets beyond the Infinity Cache.
 
 --schedules prints instead one JSON line comparing, on the shapes of SCHEDULE_SHAPES, the GEMM
 schedule the library picks (mixed 256 x 256 + 256 x 128 tiles, or 256 x 224 tiles) with the
@@ -1052,7 +1052,6 @@ def main():
     steps = args.steps
     # Timing events exist before the warmup: the first creation in a process costs tens of ms.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev = [[FenceFreeEvent() for _ in range(4)] for _ in range(steps)]
     log(f"[bench] warmup {args.warmup} steps, then at least {args.settle_seconds} s of steps; timing {steps} steps")
     # Each step's output is released before the next step runs, as in the reference's timing loop
     # (engine.py:70-92: `y = fn()` builds a lazy MLX graph, dropping the previous output, before
@@ -1074,34 +1073,49 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     total_ms = start.elapsed_time(end)
-    # Per-kernel durations: the same K steps again, each kernel recording its own start and end
-    # into a pair of events (m5k_time_next_launch: hipExtLaunchKernel on the launch stream), so no
-    # event packet sits between the quantizer and the GEMM.
-    log(f"[bench] per-kernel pass, {steps} steps")
-    hook = _lib.load().m5k_time_next_launch
-    for i in range(steps):
+    # Per-kernel durations without an event between the two kernels: any event packet there (even
+    # one without a system fence, or hipExtLaunchKernel's own pair) slows the kernels it separates
+    # (rocprofv3 kernel trace of the step, one box: quantizer 30.4 -> 31.7-33.2 us, GEMM 189.1 ->
+    # 200.2-217.7 us).  The GEMM: K launches back to back on one set of codes, one event pair around
+    # them; its average matches the GEMM's rocprof duration inside the step.  The quantizer's share
+    # of the step is the step minus that average (the two kernels run back to back, no gap between
+    # them in the kernel trace).  For reference, K quantizer launches cycling over independent
+    # activation sets beyond the Infinity Cache, each output kept for a cycle, give its streaming rate.
+    log(f"[bench] per-kernel passes, {steps} launches each")
+    aq, sa = quantize(a, "int8")
+    g0, g1 = FenceFreeEvent(), FenceFreeEvent()
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(5):
         y = None
-        hook(ev[i][0].handle, ev[i][1].handle)
-        aq, sa = quantize(a, "int8")
-        hook(ev[i][2].handle, ev[i][3].handle)
         y = gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
-        hook(None, None)
     torch.cuda.synchronize()
-    quant_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    g0.record(stream)
+    for _ in range(steps):
+        y = None
+        y = gemm(aq, wq, "int8", a_scales=sa, b_scales=ws, output_dtype=torch.bfloat16)
+    g1.record(stream)
+    torch.cuda.synchronize()
+    gemm_avg = g0.elapsed_time(g1) / steps
+    del aq, sa
+    y = None
+    n_sets = _sets_for(3 * M * K)
+    a_sets = [a] + [torch.randn((M, K), device=dev).to(torch.bfloat16) for _ in range(n_sets - 1)]
+    quant_streaming = time_streaming(torch, [lambda i=i: quantize(a_sets[i], "int8") for i in range(n_sets)],
+                                     reps=steps)
+    del a_sets
     host = []
     for _ in range(min(steps, 20)):  # synchronized host wall per step (the reference's measure)
         h0 = time.perf_counter()
-        step()
+        y = None
+        y = step()
         torch.cuda.synchronize()
         host.append((time.perf_counter() - h0) * 1e3)
     host.sort()
-    gemm_ms = [e[2].elapsed_time(e[3]) for e in ev]
     ms_per_step = max(total_ms, wall_ms) / steps
     ops = 2.0 * M * N * K
     tops = ops / (ms_per_step * 1e-3) / 1e12
-    gemm_avg = statistics.fmean(gemm_ms)
-    quant_avg = statistics.fmean(quant_ms)
     gemm_tops = ops / (gemm_avg * 1e-3) / 1e12
+    quant_avg = ms_per_step - gemm_avg
     quant_bytes = 2 * M * K + M * K + 4 * M
     quant_gbs = quant_bytes / (quant_avg * 1e-3) / 1e9
     log(f"[bench] step {ms_per_step:.4f} ms ({tops:.1f} TOPS); gemm {gemm_avg:.4f} ms ({gemm_tops:.1f} TOPS); "
@@ -1154,6 +1168,9 @@ def main():
         "kernels": {
             "quantize_rows_int8": {
                 "avg_ms": quant_avg,
+                "avg_ms_method": "step minus the GEMM's back-to-back average",
+                "streaming_ms": quant_streaming,
+                "streaming_frac_of_hbm_peak": quant_bytes / (quant_streaming * 1e-3) / 1e9 / PEAK_HBM_GBS,
                 "bound": "hbm",
                 "bytes_per_launch": quant_bytes,
                 "achieved_GBps": quant_gbs,
@@ -1166,12 +1183,13 @@ def main():
             "event_total_ms": total_ms,
             "wall_ms": wall_ms,
             "method": ("after the warmup, K steps between one pair of HIP events on the launch stream; value uses "
-                       "max(event, host wall); per-kernel averages come from a second pass of K steps in which each "
-                       "kernel records its own start and end into a pair of events (m5k_time_next_launch, "
-                       "hipExtLaunchKernel), with no event packet between the kernels"),
+                       "max(event, host wall).  Per-kernel averages, with no event between two kernels: the GEMM "
+                       "from K back-to-back launches on one set of codes between one event pair; the quantizer as "
+                       "the step minus that (kernels.quantize_rows_int8.streaming_ms: K launches cycling over "
+                       "independent activation sets beyond the Infinity Cache)"),
+            "quantizer_streaming_input_sets": n_sets,
             "host_sync_ms_per_step": {"median": host[len(host) // 2], "p10": host[len(host) // 10],
                                       "p90": host[(9 * len(host)) // 10]},
-            "gemm_p10_p90_ms": [sorted(gemm_ms)[steps // 10], sorted(gemm_ms)[(9 * steps) // 10]],
         },
     }
 

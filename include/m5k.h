@@ -185,16 +185,6 @@ int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus, int* sched
 int m5k_gemm_set_schedule(int schedule, int* previous);
 
 /*
- * Measurement hook: the calling thread's next launch of a W8A8/FP8/float GEMM kernel or of the
- * row quantizer records its own start into start_event and its end into stop_event (HIP events,
- * either may be NULL), through hipExtLaunchKernel, and the setting is consumed by that launch.
- * No counterpart in the reference; it lets a benchmark time one kernel inside a sequence without
- * queueing event packets between kernels (an event recorded between two kernels adds its own
- * processing time, and a default event also writes back and invalidates the caches).
- */
-int m5k_time_next_launch(void* start_event, void* stop_event);
-
-/*
  * Raw INT32 accumulators of the W8A8 GEMM (test hook for bit-exact parity):
  * acc[m,n] = sum_k a[m,k]*b[n,k].  Same kernel main loop as m5k_gemm_i8.
  */

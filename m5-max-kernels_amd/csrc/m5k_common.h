@@ -1,7 +1,6 @@
 // Shared device helpers and host-side error plumbing for libm5k.so (gfx950 only).
 #pragma once
 
-#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -28,23 +27,9 @@ int device_cus();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Launch-timing hook (m5k_time_next_launch): HIP events that the calling thread's next launch
-// through launch_kernel records its own start and end into (hipExtLaunchKernel), so a caller can
-// time one kernel without queueing event packets between kernels.  Consumed by that launch.
-struct LaunchTiming {
-  hipEvent_t start = nullptr, stop = nullptr;
-};
-inline thread_local LaunchTiming g_launch_timing;
-
 template <typename... KArgs, typename... Args>
 inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t st, Args&&... args) {
-  if (g_launch_timing.start != nullptr || g_launch_timing.stop != nullptr) {
-    const LaunchTiming t = g_launch_timing;
-    g_launch_timing = LaunchTiming{};
-    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, t.start, t.stop, 0, static_cast<KArgs>(args)...);
-  } else {
-    kernel<<<grid, block, 0, st>>>(static_cast<KArgs>(args)...);
-  }
+  kernel<<<grid, block, 0, st>>>(static_cast<KArgs>(args)...);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

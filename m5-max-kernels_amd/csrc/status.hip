@@ -47,9 +47,3 @@ int device_cus() {
 extern "C" const char* m5k_last_error(void) { return m5k::g_error; }
 
 extern "C" int m5k_abi_version(void) { return 100; }
-
-extern "C" int m5k_time_next_launch(void* start_event, void* stop_event) {
-  m5k::clear_error();
-  m5k::g_launch_timing = m5k::LaunchTiming{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
-  return M5K_OK;
-}

@@ -50,7 +50,6 @@ SIGNATURES = {
     "m5k_gemm_i8_acc": [_p, _p, _i64, _i64, _i64, _p, _p],
     "m5k_gemm_launch_plan": [_i32, _i64, _i64, _i32, _p, _p],
     "m5k_gemm_set_schedule": [_i32, _p],
-    "m5k_time_next_launch": [_p, _p],
     "m5k_gemm_i8_splitk": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _i32, _p, _i64, _p],
     "m5k_gemm_i8_splitk_noalloc": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _i32, _p],
     "m5k_gemm_f8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p],
