@@ -851,6 +851,9 @@ def _diag_lib():
     lib.m5k_diag_mfma_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                           ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                           ctypes.c_void_p]
+    lib.m5k_diag_stream_mix.restype = ctypes.c_int
+    lib.m5k_diag_stream_mix.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -911,6 +914,120 @@ def mfma_ceiling(torch, dev, rounds=8, reps=10):
                     "p10_p90_us": [sorted(v)[len(v) // 10] * 1e3, sorted(v)[(9 * len(v)) // 10] * 1e3]}
         log(f"[bench] mfma ceiling: {key} {ms * 1e3:.1f} us = {tops:.0f} TOPS ({tops / PEAK_INT8_TOPS:.3f})")
     res["gemm_frac_of_ceiling"] = res["mfma_ceiling_16x16x64"]["us"] / res["gemm_i8"]["us"]
+    res["quad_vs_eight_waves"] = quad_probe(torch, dev, aq, wq, sa, ws, rounds, reps)
+    return res
+
+
+def quad_probe(torch, dev, aq, wq, sa, ws, rounds, reps):
+    """The four-wave grid (forced quad schedule: 128 x 128 per wave, one wave per SIMD) against the
+    library's eight-wave launch on the FFN-down codes, FFN-up and 4096^3 (seeded INT8 codes):
+    bit equality, then ABBA rounds of `reps` launches between one event pair, queued behind a
+    short GPU spin; medians."""
+    from m5kernels_amd import gemm
+    from m5kernels_amd.hip import launch_override
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    up_a = torch.randint(-127, 128, (4096, 4096), generator=g, device=dev, dtype=torch.int8)
+    up_w = torch.randint(-127, 128, (16384, 4096), generator=g, device=dev, dtype=torch.int8)
+    up_sa = torch.rand(4096, generator=g, device=dev) * 0.01 + 1e-3
+    up_ws = torch.rand(16384, generator=g, device=dev) * 0.01 + 1e-3
+    shapes = {"ffn_down_4096x4096x16384": (aq, wq, sa, ws), "ffn_up_4096x16384x4096": (up_a, up_w, up_sa, up_ws),
+              "q_4096x4096x4096": (up_a, up_w[:4096], up_sa, up_ws[:4096])}
+    out = {}
+    for name, (a, w, s_a, s_w) in shapes.items():
+        def run(quad, a=a, w=w, s_a=s_a, s_w=s_w):
+            if quad:
+                with launch_override("quad"):
+                    return gemm(a, w, "int8", a_scales=s_a, b_scales=s_w, output_dtype=torch.bfloat16)
+            with launch_override("plain"):
+                return gemm(a, w, "int8", a_scales=s_a, b_scales=s_w, output_dtype=torch.bfloat16)
+
+        same = bool(torch.equal(run(False).view(torch.int16), run(True).view(torch.int16)))
+        settle(torch, lambda: run(False), 0.2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = {False: [], True: []}
+        for r in range(rounds):
+            for quad in ((False, True) if r % 2 == 0 else (True, False)):
+                torch.cuda._sleep(2_000_000)  # the host queues every launch before the first runs
+                e0.record()
+                for _ in range(reps):
+                    run(quad)
+                e1.record()
+                torch.cuda.synchronize()
+                times[quad].append(e0.elapsed_time(e1) / reps)
+        eight, quad = statistics.median(times[False]) * 1e3, statistics.median(times[True]) * 1e3
+        out[name] = {"bit_identical": same, "eight_waves_us": eight, "quad_us": quad, "quad_over_eight": quad / eight}
+        log(f"[bench] quad vs eight waves: {name} {eight:.1f} / {quad:.1f} us (x{quad / eight:.3f}), "
+            f"bit-identical {same}")
+    return out
+
+
+# Traffic mixes of the row kernels for hbm_ceiling: (name, rows, K, inputs, full-size output).
+# Every mix writes the INT8 codes (half the BF16 input's bytes).
+STREAM_MIXES = (
+    ("quantize_ffn_down", M, K, 1, False),      # A bf16 -> codes
+    ("prep_ungated_m4096", 4096, 4096, 1, False),  # X -> codes
+    ("prep_gated_m4096", 4096, 4096, 2, True),     # X, branch -> R_next, codes
+    ("prep_gated_m9914", 9914, 4096, 2, True),
+)
+
+
+def hbm_ceiling(torch, dev, grid_blocks=2048):
+    """--hbm-ceiling: the HBM rate of each row kernel's read/write mix with no compute
+    (libm5k_diag.so's stream_mix: 16-byte loads, one XOR, 16- and 8-byte stores), timed like the
+    row kernels: time_op on one repeated input set and time_streaming over independent sets.
+    The row kernels' parameter tables and per-row scales (under 3% of their bytes) are left out."""
+    import ctypes
+
+    lib = _diag_lib()
+    res = {"grid_blocks": grid_blocks}
+
+    def launcher(x, b, full, half):
+        def run():
+            stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+            rc = lib.m5k_diag_stream_mix(x.data_ptr(), None if b is None else b.data_ptr(),
+                                         None if full is None else full.data_ptr(), half.data_ptr(), x.numel() // 8,
+                                         grid_blocks, stream)
+            if rc != 0:
+                raise RuntimeError(f"m5k_diag_stream_mix failed ({rc})")
+        return run
+
+    for name, rows, k, n_in, full_out in STREAM_MIXES:
+        nbytes = rows * k * (2 * n_in + (2 if full_out else 0) + 1)
+
+        def make_set():
+            x = torch.randint(-2**15, 2**15, (rows, k), dtype=torch.int16, device=dev).view(torch.bfloat16)
+            b = torch.randint(-2**15, 2**15, (rows, k), dtype=torch.int16, device=dev).view(torch.bfloat16) \
+                if n_in == 2 else None
+            full = torch.empty((rows, k), dtype=torch.bfloat16, device=dev) if full_out else None
+            half = torch.empty((rows, k), dtype=torch.int8, device=dev)
+            return x, b, full, half
+
+        s0 = make_set()
+        x, b, full, half = s0
+        launcher(*s0)()
+        torch.cuda.synchronize()
+        xw = x.view(torch.int16).view(-1, 8)
+        bw = b.view(torch.int16).view(-1, 8) if b is not None else torch.zeros_like(xw)
+        r = xw ^ bw
+        if full is not None:
+            assert torch.equal(full.view(torch.int16).view(-1, 8), r), name
+        r32 = r.view(torch.int32)
+        h = torch.stack([r32[:, 0] ^ r32[:, 1], r32[:, 2] ^ r32[:, 3]], 1)
+        assert torch.equal(half.view(torch.int32).view(-1, 2), h), name
+        del xw, bw, r, r32, h
+        one = time_op(torch, launcher(*s0))["avg_ms"]
+        n = _sets_for(nbytes)
+        sets = [s0] + [make_set() for _ in range(n - 1)]
+        st = time_streaming(torch, [launcher(*st_) for st_ in sets])
+        del sets, s0, x, b, full, half
+        gbs = lambda t: nbytes / (t * 1e-3) / 1e9  # noqa: E731
+        res[name] = {"bytes": nbytes, "one_set_us": one * 1e3, "one_set_GBps": gbs(one),
+                     "one_set_frac_of_hbm_peak": gbs(one) / PEAK_HBM_GBS, "streaming_us": st * 1e3,
+                     "streaming_GBps": gbs(st), "streaming_frac_of_hbm_peak": gbs(st) / PEAK_HBM_GBS,
+                     "streaming_input_sets": n}
+        log(f"[bench] hbm ceiling: {name} {nbytes / 1e6:.1f} MB one set {one * 1e3:.1f} us "
+            f"({gbs(one) / PEAK_HBM_GBS:.3f}), streaming {st * 1e3:.1f} us ({gbs(st) / PEAK_HBM_GBS:.3f})")
     return res
 
 
@@ -991,6 +1108,8 @@ def main():
                    help="REPS mixed-dtype gated prep calls (one dispatch each), then their timing; prints nothing else")
     p.add_argument("--mfma-ceiling", action="store_true",
                    help="only time the FFN-down GEMM beside MFMA-only kernels on its own codes (the ceiling)")
+    p.add_argument("--hbm-ceiling", action="store_true",
+                   help="only time each row kernel's read/write mix with no compute (one set and streaming)")
     p.add_argument("--counter-workload", type=int, default=0, metavar="REPS",
                    help="only launch each profiled kernel REPS times (for rocprofv3 --pmc runs)")
     p.add_argument("--op-settle", type=float, default=OP_SETTLE_S,
@@ -1027,6 +1146,9 @@ def main():
         return
     if args.prep_mixed:
         print(json.dumps({"prep_mixed": prep_mixed(torch, dev, args.prep_mixed)}))
+        return
+    if args.hbm_ceiling:
+        print(json.dumps({"hbm_ceiling": hbm_ceiling(torch, dev)}))
         return
     if args.counter_workload:
         counter_workload(torch, dev, args.counter_workload)

@@ -164,6 +164,7 @@ int m5k_gemm_i8_splitk_noalloc(const int8_t* a, const int8_t* b, int64_t m, int6
  *   1  mixed: the leading *full_tiles 256 x 256 tiles (whole rounds), every other tile as
  *      two 256 x 128 halves in the same launch;
  *   2  narrow: 256 x 224 tiles (I8 / BF16 / F16 only);
+ *   3  quad: 256 x 256 tiles on four waves of 128 x 128 (I8 only; only when forced, below);
  * and *full_tiles is -1 unless the schedule is 1.  Every m5k_gemm_* entry point makes this
  * choice with the device's CU count for operands on the direct-to-LDS path (row bytes a
  * multiple of 16, 16-byte aligned bases); the others run the plain schedule.  Results are
@@ -174,12 +175,13 @@ int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus, int* sched
 
 /*
  * Force the schedule of the MFMA GEMM launches made by the calling host thread: -1 restores the
- * library's own plan (m5k_gemm_launch_plan), 0 plain, 1 mixed, 2 narrow (plain for FP8/FP32).
+ * library's own plan (m5k_gemm_launch_plan), 0 plain, 1 mixed, 2 narrow (plain for FP8/FP32),
+ * 3 quad (plain for all but I8; never the library's own choice, as it measured slower).
  * *previous (may be NULL) receives the thread's earlier setting.  No counterpart in the
  * reference, whose tuner searches Metal threadgroup tiles through gemm's `tile` argument
  * (src/m5kernels/cli.py:66-151); this is the gfx950 knob the harness tuner searches instead.
  * The setting is thread-local, so other host threads keep their own plan; for tools outside the
- * process, M5K_GEMM_SCHEDULE=plain|mixed|narrow in the environment does the same when no thread
+ * process, M5K_GEMM_SCHEDULE=plain|mixed|narrow|quad in the environment does the same when no thread
  * setting is made.  Results are bit-identical under every schedule.
  */
 int m5k_gemm_set_schedule(int schedule, int* previous);

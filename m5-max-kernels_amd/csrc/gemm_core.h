@@ -190,7 +190,16 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // Issued as inline asm so the compiler does not serialize it against LDS reads of other
 // stage buffers; every consumer waits with an explicit vmcnt and a barrier instead.  The
 // main loop issues no other vector-memory instruction, so those explicit counts are exact.
+// lds_base and rsrc are wave-uniform by construction.  UNIFORM states it with readfirstlane, so
+// that they stay in SGPRs (the asm's "s" operands) where the compiler cannot prove it (the
+// four-wave grid, whose 256 accumulators leave it under register pressure).
+template <bool UNIFORM = false>
 __device__ __forceinline__ void dma16(uint32_t lds_base, uint32_t voffset, v4i rsrc) {
+  if constexpr (UNIFORM) {
+    rsrc = v4i{__builtin_amdgcn_readfirstlane(rsrc[0]), __builtin_amdgcn_readfirstlane(rsrc[1]),
+               __builtin_amdgcn_readfirstlane(rsrc[2]), __builtin_amdgcn_readfirstlane(rsrc[3])};
+    lds_base = __builtin_amdgcn_readfirstlane(lds_base);
+  }
   __asm__ volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
@@ -457,8 +466,8 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
     for (int q = q0; q < q1; ++q) {
       const bool is_b = q < 2 * NPAIR ? (q & 1) != 0 : G::DMA_INSTR_B > G::DMA_INSTR;
       const int i = q < 2 * NPAIR ? q >> 1 : q - NPAIR;
-      if (!is_b) dma16(la + 8 * i * BKB, a_base[i] | kill[i & 1], ra);
-      else dma16(lb + 8 * i * BKB, b_base[i] | kill[i & 1], rb);
+      if (!is_b) dma16<G::WAVES == 4>(la + 8 * i * BKB, a_base[i] | kill[i & 1], ra);
+      else dma16<G::WAVES == 4>(lb + 8 * i * BKB, b_base[i] | kill[i & 1], rb);
     }
   };
   auto dma = [&](uint8_t* sa, uint8_t* sb, int64_t kr) { dma_range(sa, sb, kr, 0, NQ); };
@@ -607,20 +616,30 @@ struct AccGeom {
   __device__ __forceinline__ int col(int j) const { return c0 + j * MD; }
 };
 
-// A tile's row and column scales, one per thread (threads [0, BM) the rows, [BM, BM + TN) the
-// columns; 0 past the matrix), loaded before the main loop so that their latency hides behind it
-// instead of opening the epilogue: 0.1-0.7 us less per tile round (A/B, same bits: 4096^3
-// 56.1 -> 55.4 us, FFN-up 211.0 -> 209.1 us).  The load is issued before the loop's first DMA,
-// so the loop's in-order vmcnt waits cover it and their counts stay exact.
+// A tile's row and column scales, PER per thread (scale t on thread t % THREADS; [0, BM) the
+// rows, [BM, BM + TN) the columns; 0 past the matrix), loaded before the main loop so that
+// their latency hides behind it instead of opening the epilogue: 0.1-0.7 us less per tile
+// round (A/B, same bits: 4096^3 56.1 -> 55.4 us, FFN-up 211.0 -> 209.1 us).  The loads are
+// issued before the loop's first DMA, so the loop's in-order vmcnt waits cover them and their
+// counts stay exact.
 template <class G>
 struct TileScalePrefetch {
-  static_assert(G::THREADS >= BM + G::TN, "one scale per thread");
-  float v;
+  static constexpr int PER = (BM + G::TN + G::THREADS - 1) / G::THREADS;  // scales per thread
+  float v[PER];
   __device__ __forceinline__ TileScalePrefetch(const float* __restrict__ sa, const float* __restrict__ sb, int M,
                                                int N, int m0, int n0) {
-    const int t = threadIdx.x;
-    const int m = m0 + t, n = n0 + t - BM;
-    v = t < BM ? (m < M ? sa[m] : 0.0f) : (t < BM + G::TN && n < N ? sb[n] : 0.0f);
+    if constexpr (PER == 1) {
+      // One scale per thread: a single load from either vector (the eight-wave grids).
+      const int t = threadIdx.x;
+      const int m = m0 + t, n = n0 + t - BM;
+      v[0] = t < BM ? (m < M ? sa[m] : 0.0f) : (t < BM + G::TN && n < N ? sb[n] : 0.0f);
+    } else {
+      // Thread t takes row scale t and column scale t (PER == 2: BM == TN == THREADS).
+      static_assert(PER == 2 && G::THREADS == BM && G::TN == BM, "two scales per thread: one row, one column");
+      const int t = threadIdx.x;
+      v[0] = m0 + t < M ? sa[m0 + t] : 0.0f;
+      v[1] = n0 + t < N ? sb[n0 + t] : 0.0f;
+    }
   }
 };
 
@@ -643,7 +662,11 @@ struct TileScales {
   }
   __device__ __forceinline__ TileScales(const TileScalePrefetch<G>& pre, int tid) {
     float* w = reinterpret_cast<float*>(g_lds + EPI_SCALES_OFFSET);
-    if (tid < BM + G::TN) w[tid] = pre.v;
+#pragma unroll
+    for (int i = 0; i < TileScalePrefetch<G>::PER; ++i) {
+      const int t = tid + i * G::THREADS;
+      if (t < BM + G::TN) w[t] = pre.v[i];
+    }
     __syncthreads();
     s = w;
   }

@@ -56,13 +56,13 @@ extern "C" int m5k_gemm_launch_plan(int ab_dtype, int64_t m, int64_t n, int cus,
                   ab_dtype == M5K_F32,
               "%s: ab_dtype must be I8, U8 (FP8 codes), BF16, F16 or F32", name);
   const bool md16 = ab_dtype == M5K_I8 || ab_dtype == M5K_BF16 || ab_dtype == M5K_F16;
-  *schedule = plan_schedule(md16, m, n, cus, *full_tiles);
+  *schedule = plan_schedule(md16, ab_dtype == M5K_I8, m, n, cus, *full_tiles);
   return M5K_OK;
 }
 
 extern "C" int m5k_gemm_set_schedule(int schedule, int* previous) {
   clear_error();
-  M5K_REQUIRE(schedule >= -1 && schedule <= SCHED_NARROW, "m5k_gemm_set_schedule: schedule %d outside [-1, 2]",
+  M5K_REQUIRE(schedule >= -1 && schedule <= SCHED_QUAD, "m5k_gemm_set_schedule: schedule %d outside [-1, 3]",
               schedule);
   if (previous) *previous = g_thread_schedule;
   g_thread_schedule = schedule;

@@ -342,15 +342,20 @@ inline bool dma_ok(const void* a, const void* b, int64_t kb) {
   return kb % 16 == 0 && kb <= (int64_t(1) << 23) && aligned16(a) && aligned16(b);
 }
 
-enum Schedule { SCHED_PLAIN = 0, SCHED_MIXED = 1, SCHED_NARROW = 2 };
+// SCHED_QUAD: plain 256 x 256 tiles on Grid4 (four waves of 128 x 128, one per SIMD, 256 AGPR
+// accumulators), W8A8 only.  Never planned: on the FFN-down, FFN-up and 4096^3 GEMMs it measured
+// 1.10-1.15x the time of the eight-wave grid (same bits), since a lone wave per SIMD has no
+// sibling to issue MFMAs while it waits on LDS reads and stage barriers.  It stays a tuner option.
+enum Schedule { SCHED_PLAIN = 0, SCHED_MIXED = 1, SCHED_NARROW = 2, SCHED_QUAD = 3 };
 
 // A schedule forced for the calls of this host thread (m5k_gemm_set_schedule: the harness tuner),
-// else one named by M5K_GEMM_SCHEDULE ("plain", "mixed", "narrow"; read on every call, for outside
-// tools), else -1.  A forced mixed launch keeps the planner's full-tile count when it has one, else
-// runs every tile of the last (or only) round as two halves.
+// else one named by M5K_GEMM_SCHEDULE ("plain", "mixed", "narrow", "quad"; read on every call, for
+// outside tools), else -1.  A forced mixed launch keeps the planner's full-tile count when it has
+// one, else runs every tile of the last (or only) round as two halves.  Narrow applies to the
+// 16 x 16 modes and quad to W8A8; the other modes run plain in their place.
 inline thread_local int g_thread_schedule = -1;
 
-inline int forced_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& full) {
+inline int forced_schedule(bool md16, bool i8, int64_t m, int64_t n, int cus, int64_t& full) {
   int which = g_thread_schedule;
   if (which < 0) {
     const char* env = std::getenv("M5K_GEMM_SCHEDULE");
@@ -358,11 +363,13 @@ inline int forced_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& fu
     if (std::strcmp(env, "plain") == 0) which = SCHED_PLAIN;
     else if (std::strcmp(env, "mixed") == 0) which = SCHED_MIXED;
     else if (std::strcmp(env, "narrow") == 0) which = SCHED_NARROW;
+    else if (std::strcmp(env, "quad") == 0) which = SCHED_QUAD;
     else return -1;
   }
   full = -1;
   if (which == SCHED_PLAIN) return SCHED_PLAIN;
   if (which == SCHED_NARROW) return md16 ? SCHED_NARROW : SCHED_PLAIN;
+  if (which == SCHED_QUAD) return i8 ? SCHED_QUAD : SCHED_PLAIN;
   if (which == SCHED_MIXED && cus >= XCDS && cus % XCDS == 0) {
     const int64_t total = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     full = mixed_full_tiles(m, n, cus);
@@ -374,8 +381,8 @@ inline int forced_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& fu
 
 // Launch schedule of an aligned GEMM with an [m, n] output on `cus` CUs; `full` receives the
 // mixed launch's full tiles (-1 otherwise).  Narrow tiles exist for the 16 x 16 modes only.
-inline int plan_schedule(bool md16, int64_t m, int64_t n, int cus, int64_t& full) {
-  if (const int forced = forced_schedule(md16, m, n, cus, full); forced >= 0) return forced;
+inline int plan_schedule(bool md16, bool i8, int64_t m, int64_t n, int cus, int64_t& full) {
+  if (const int forced = forced_schedule(md16, i8, m, n, cus, full); forced >= 0) return forced;
   full = mixed_full_tiles(m, n, cus);
   if (md16 && narrow_pays(m, n, cus, full)) {
     full = -1;
@@ -399,13 +406,20 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   q.coalesced = n % 8 == 0 && aligned16(p.c) && (p.residual == nullptr || (aligned16(p.residual) && aligned16(p.gate)));
   if (aligned) {
     int64_t full = -1;
-    const int sched = plan_schedule(Traits<MODE>::MD == 16, m, n, device_cus(), full);
+    const int sched = plan_schedule(Traits<MODE>::MD == 16, MODE == I8, m, n, device_cus(), full);
     if constexpr (Traits<MODE>::MD == 16) {
       if (sched == SCHED_NARROW) {
         using G = Grid8Narrow;
         const int64_t wgs = ((m + BM - 1) / BM) * ((n + G::TN - 1) / G::TN);
         launch_kernel(gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW, G>, dim3(static_cast<unsigned>(wgs)), block, st,
                       A, B, (int)m, (int)n, kb, q);
+        return launch_status(name);
+      }
+    }
+    if constexpr (MODE == I8) {
+      if (sched == SCHED_QUAD) {
+        launch_kernel(gemm_kernel<MODE, true, OUT_DT, BIAS, GATE, RAW, Grid4>, grid, dim3(Grid4::THREADS), st, A, B,
+                      (int)m, (int)n, kb, q);
         return launch_status(name);
       }
     }

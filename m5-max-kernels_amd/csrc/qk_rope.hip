@@ -486,7 +486,7 @@ int launch_fused(const void* a, const void* b, int64_t m, int64_t n, int64_t k, 
     // The GEMM library's schedule for this output shape; 256 x 224 tiles do not hold whole
     // heads, so the narrow schedule is not offered here.
     int64_t full = -1;
-    if (gemm::detail::plan_schedule(false, m, n, device_cus(), full) == gemm::detail::SCHED_MIXED) {
+    if (gemm::detail::plan_schedule(false, false, m, n, device_cus(), full) == gemm::detail::SCHED_MIXED) {
       const int64_t wgs = full + 2 * (tiles - full);
       qk_mixed_kernel<MODE><<<dim3(static_cast<unsigned>(wgs)), block, 0, st>>>(A, B, (int)m, (int)n, kb,
                                                                                static_cast<int>(full), sa, sb, p, fast);

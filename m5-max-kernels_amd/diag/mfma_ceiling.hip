@@ -10,7 +10,11 @@
 // distribution, so its duration bounds what the matrix cores deliver at the clock the chip holds
 // on that data.  `constant` replaces every code with 1 (the low-power case).  The one-wave form
 // (md = 4) runs the same MFMA stream as 4 waves, one per SIMD, each doing the work of two: it
-// measures what a single wave's back-to-back 16 x 16 x 64 MFMAs can issue.
+// measures what a single wave's back-to-back 16 x 16 x 64 MFMAs can issue.  Both forms are
+// compiled for two waves per SIMD (at most 256 VGPRs), so each loop holds its MFMAs and nothing
+// else.  (Compiled for one wave per SIMD, the one-wave loop gained 192 accumulator moves per 64
+// MFMAs.)  The one-wave form is launched with 96 KiB of dynamic LDS that it never touches, so that
+// a CU (160 KiB) holds one of its workgroups.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -22,7 +26,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 template <int MD, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, 1) void mfma_ceiling_kernel(const int8_t* __restrict__ A,
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void mfma_ceiling_kernel(const int8_t* __restrict__ A,
                                                               const int8_t* __restrict__ B, int tiles_n,
                                                               int64_t kb, int iters, int constant,
                                                               int32_t* __restrict__ out) {
@@ -96,6 +100,6 @@ extern "C" int m5k_diag_mfma_ceiling(const int8_t* a, const int8_t* b, int64_t m
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (md == 16) mfma_ceiling_kernel<16, 8><<<grid, block, 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
   else if (md == 32) mfma_ceiling_kernel<32, 8><<<grid, block, 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
-  else mfma_ceiling_kernel<16, 4><<<grid, dim3(256), 0, st>>>(a, b, tiles_n, kb, iters, constant, out);
+  else mfma_ceiling_kernel<16, 4><<<grid, dim3(256), 96 * 1024, st>>>(a, b, tiles_n, kb, iters, constant, out);
   return static_cast<int>(hipGetLastError());
 }

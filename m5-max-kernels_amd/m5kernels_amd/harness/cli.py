@@ -48,7 +48,7 @@ _DISTRIBUTIONS = ("normal", "outliers", "zeros")
 class Launch:
     """One gfx950 GEMM launch choice; None fields keep the library's plan."""
 
-    schedule: str | None = None  # "plain" | "mixed" | "narrow"
+    schedule: str | None = None  # "plain" | "mixed" | "narrow" | "quad"
     splits: int | None = None  # W8A8 split-K count (1 = no split)
 
     def record(self):
@@ -74,6 +74,8 @@ def launch_space(case, precision, cus=256):
     space = [Launch(), Launch("plain"), Launch("mixed")]
     if precision in ("int8", "bf16", "fp16", "mxint8"):
         space.append(Launch("narrow"))  # 256 x 224 tiles exist for the 16 x 16 MFMA modes
+    if precision == "int8":
+        space.append(Launch("quad"))  # four waves of 128 x 128, W8A8 only
     if precision == "int8" and case.get("k", 0) % 16 == 0:
         m, n, k = case["m"], case["n"], case["k"]
         planned = splitk_plan(m, n, k, cus)

@@ -154,7 +154,7 @@ def tail_split_plan(m, n, k, cus=256):
 
 
 _PLAN_DTYPES = {"int8": _lib.I8, "fp8": _lib.U8, "bf16": _lib.BF16, "fp16": _lib.F16, "fp32": _lib.F32}
-SCHEDULES = ("plain", "mixed", "narrow")
+SCHEDULES = ("plain", "mixed", "narrow", "quad")
 
 _override = threading.local()
 
@@ -165,7 +165,7 @@ _SCHEDULE_CODES = {name: i for i, name in enumerate(SCHEDULES)}
 @contextlib.contextmanager
 def launch_override(schedule=None, splits=None):
     """Fix the gfx950 GEMM launch for the calls this thread makes inside the block: `schedule`
-    ("plain", "mixed" or "narrow"; set in the library for this host thread with
+    ("plain", "mixed", "narrow" or "quad"; set in the library for this host thread with
     m5k_gemm_set_schedule) and, for the W8A8 linear, the split-K count `splits` (1: no split;
     the INT32 partials are exact, so every choice gives the same bits).  A forced schedule with
     `splits` None runs unsplit: the launch timed is the one named.  None keeps the library's own
@@ -192,7 +192,7 @@ def launch_override(schedule=None, splits=None):
 
 def launch_plan(mode, m, n, cus=256):
     """The library's GEMM schedule for an [m, n] output on `cus` CUs (m5k_gemm_launch_plan;
-    host only): ("plain" | "mixed" | "narrow", full tiles of the mixed launch or -1)."""
+    host only): ("plain" | "mixed" | "narrow" | "quad", full tiles of the mixed launch or -1)."""
     sched, full = ctypes.c_int(0), ctypes.c_int64(0)
     _lib.call("m5k_gemm_launch_plan", _PLAN_DTYPES[mode], m, n, cus, ctypes.byref(sched), ctypes.byref(full))
     return SCHEDULES[sched.value], full.value

@@ -245,6 +245,22 @@ def test_launch_plan_decisions(monkeypatch):
         launch_plan("int8", 9914, 4096, 0)
 
 
+def test_forced_quad_schedule_plan(monkeypatch):
+    """The four-wave (quad) schedule is never the library's own choice; forced, it applies to
+    W8A8 only and the other modes run plain (host query, no GPU)."""
+    from m5kernels_amd.hip import launch_override, launch_plan
+
+    for shape in ((4096, 4096), (9914, 4096), (4096, 7168)):
+        assert launch_plan("int8", *shape, 256)[0] != "quad"
+    with launch_override("quad"):
+        assert launch_plan("int8", 9914, 4096, 256) == ("quad", -1)
+        assert launch_plan("bf16", 4096, 7168, 256) == ("plain", -1)
+        assert launch_plan("fp8", 4096, 4096, 256) == ("plain", -1)
+    monkeypatch.setenv("M5K_GEMM_SCHEDULE", "quad")
+    assert launch_plan("int8", 4096, 7168, 256) == ("quad", -1)
+    assert launch_plan("fp32", 9914, 4096, 256) == ("plain", -1)
+
+
 def test_tail_split_plan_decisions():
     """Host schedule of the W8A8 linear on 256 CUs: the row split is taken where the measured
     cost model says it pays (H3 widths at M 4096) and declined where it does not (M 9914 x

@@ -95,6 +95,6 @@ def test_schedule_setting_is_thread_local():
 
 def test_set_schedule_rejects_unknown_codes():
     lib = _lib.load()
-    assert lib.m5k_gemm_set_schedule(3, None) != 0
+    assert lib.m5k_gemm_set_schedule(4, None) != 0
     assert lib.m5k_gemm_set_schedule(-2, None) != 0
     assert _thread_schedule() == -1

@@ -30,10 +30,11 @@ def _codes(m, n, k, seed=83, bound=127):
     return a, b, sa, sb
 
 
-@pytest.fixture(params=["auto", "plain"])
+@pytest.fixture(params=["auto", "plain", "quad"])
 def schedule(request, monkeypatch):
     """Run a test under the library's launch choice ("auto": shapes with a partial last round
-    take the mixed 256 x 256 / 256 x 128 launch or 256 x 224 tiles) and with both switched off."""
+    take the mixed 256 x 256 / 256 x 128 launch or 256 x 224 tiles), with both switched off, and
+    with the four-wave grid forced (W8A8; the other modes run plain under it)."""
     _set_schedule(monkeypatch, request.param)
     return request.param
 
@@ -44,6 +45,10 @@ def _set_schedule(monkeypatch, schedule):
             monkeypatch.setenv(var, "0")
         else:
             monkeypatch.delenv(var, raising=False)
+    if schedule == "quad":
+        monkeypatch.setenv("M5K_GEMM_SCHEDULE", "quad")
+    else:
+        monkeypatch.delenv("M5K_GEMM_SCHEDULE", raising=False)
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -447,6 +452,31 @@ def test_mixed_tiles_float_modes_bit_identical(shape, mode, monkeypatch, device)
     plain = gemm(a, b, mode, **kw)
     view = torch.int16 if mixed.element_size() == 2 else torch.int32
     assert torch.equal(mixed.view(view), plain.view(view))
+
+
+@pytest.mark.parametrize("epilogue", ["scales", "bias_table", "gated"])
+@pytest.mark.parametrize("shape", [(1000, 700, 528), (4096, 1280, 2048), (513, 4100, 1040)])
+def test_quad_schedule_bit_identical_to_plain(shape, epilogue, monkeypatch, device):
+    """The four-wave grid (forced quad schedule) against the eight-wave plain launch, with the
+    scale, bias-table and gated epilogues, on ragged and multi-round shapes."""
+    m, n, k = shape
+    print(f"case m={m} n={n} k={k} {epilogue}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(m + n + k)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8).to(device)
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(device)
+    kw = dict(a_scales=(torch.rand(m, generator=g) + 0.5).to(device),
+              b_scales=(torch.rand(n, generator=g) * 0.01 + 0.001).to(device), output_dtype=torch.bfloat16)
+    if epilogue == "bias_table":
+        kw.update(bias=torch.randn((3, n), generator=g).to(device),
+                  bias_row_map=(torch.arange(m, dtype=torch.int32) % 3).to(device))
+    elif epilogue == "gated":
+        kw.update(residual=torch.randn((m, n), generator=g).to(torch.bfloat16).to(device),
+                  gate=torch.randn((n,), generator=g).to(torch.bfloat16).to(device))
+    _set_schedule(monkeypatch, "plain")
+    plain = gemm(a, b, "int8", **kw)
+    _set_schedule(monkeypatch, "quad")
+    quad = gemm(a, b, "int8", **kw)
+    assert torch.equal(quad.view(torch.int16), plain.view(torch.int16))
 
 
 def _random_schedule_cases(count_per_schedule=20, seed=2024):

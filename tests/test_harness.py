@@ -214,11 +214,11 @@ def test_tune_launch_space():
     (narrow only for the 16 x 16 MFMA modes) and, for INT8, split-K counts."""
     case = {"id": "c", "op": "gemm", "m": 128, "n": 4096, "k": 16384}
     int8 = cli.launch_space(case, "int8")
-    assert int8[0] == cli.Launch() and cli.Launch("narrow") in int8
+    assert int8[0] == cli.Launch() and cli.Launch("narrow") in int8 and cli.Launch("quad") in int8
     splits = sorted(l.splits for l in int8 if l.splits)
     assert splits and all(2 <= s <= 64 for s in splits)
     fp8 = cli.launch_space(case, "fp8")
-    assert cli.Launch("narrow") not in fp8 and not any(l.splits for l in fp8)
+    assert cli.Launch("narrow") not in fp8 and cli.Launch("quad") not in fp8 and not any(l.splits for l in fp8)
     assert len(set(int8)) == len(int8)
     for launch in int8:
         assert cli.Launch.from_record(launch.record()) == launch
