@@ -853,7 +853,7 @@ def _diag_lib():
                                           ctypes.c_void_p]
     lib.m5k_diag_stream_mix.restype = ctypes.c_int
     lib.m5k_diag_stream_mix.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                                        ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+                                        ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -972,22 +972,26 @@ STREAM_MIXES = (
 )
 
 
+STREAM_POLICIES = ("plain", "nt_stores", "nt_loads_stores")
+
+
 def hbm_ceiling(torch, dev, grid_blocks=2048):
     """--hbm-ceiling: the HBM rate of each row kernel's read/write mix with no compute
     (libm5k_diag.so's stream_mix: 16-byte loads, one XOR, 16- and 8-byte stores), timed like the
-    row kernels: time_op on one repeated input set and time_streaming over independent sets.
+    row kernels: time_op on one repeated input set and time_streaming over independent sets,
+    for each cache policy of STREAM_POLICIES; the top-level figures are the fastest policy's.
     The row kernels' parameter tables and per-row scales (under 3% of their bytes) are left out."""
     import ctypes
 
     lib = _diag_lib()
     res = {"grid_blocks": grid_blocks}
 
-    def launcher(x, b, full, half):
+    def launcher(x, b, full, half, policy=0):
         def run():
             stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
             rc = lib.m5k_diag_stream_mix(x.data_ptr(), None if b is None else b.data_ptr(),
                                          None if full is None else full.data_ptr(), half.data_ptr(), x.numel() // 8,
-                                         grid_blocks, stream)
+                                         grid_blocks, policy, stream)
             if rc != 0:
                 raise RuntimeError(f"m5k_diag_stream_mix failed ({rc})")
         return run
@@ -1005,29 +1009,38 @@ def hbm_ceiling(torch, dev, grid_blocks=2048):
 
         s0 = make_set()
         x, b, full, half = s0
-        launcher(*s0)()
-        torch.cuda.synchronize()
         xw = x.view(torch.int16).view(-1, 8)
         bw = b.view(torch.int16).view(-1, 8) if b is not None else torch.zeros_like(xw)
         r = xw ^ bw
-        if full is not None:
-            assert torch.equal(full.view(torch.int16).view(-1, 8), r), name
         r32 = r.view(torch.int32)
         h = torch.stack([r32[:, 0] ^ r32[:, 1], r32[:, 2] ^ r32[:, 3]], 1)
-        assert torch.equal(half.view(torch.int32).view(-1, 2), h), name
+        for policy in range(len(STREAM_POLICIES)):
+            if full is not None:
+                full.zero_()
+            half.zero_()
+            launcher(*s0, policy)()
+            torch.cuda.synchronize()
+            if full is not None:
+                assert torch.equal(full.view(torch.int16).view(-1, 8), r), (name, policy)
+            assert torch.equal(half.view(torch.int32).view(-1, 2), h), (name, policy)
         del xw, bw, r, r32, h
-        one = time_op(torch, launcher(*s0))["avg_ms"]
         n = _sets_for(nbytes)
         sets = [s0] + [make_set() for _ in range(n - 1)]
-        st = time_streaming(torch, [launcher(*st_) for st_ in sets])
-        del sets, s0, x, b, full, half
         gbs = lambda t: nbytes / (t * 1e-3) / 1e9  # noqa: E731
-        res[name] = {"bytes": nbytes, "one_set_us": one * 1e3, "one_set_GBps": gbs(one),
-                     "one_set_frac_of_hbm_peak": gbs(one) / PEAK_HBM_GBS, "streaming_us": st * 1e3,
-                     "streaming_GBps": gbs(st), "streaming_frac_of_hbm_peak": gbs(st) / PEAK_HBM_GBS,
-                     "streaming_input_sets": n}
-        log(f"[bench] hbm ceiling: {name} {nbytes / 1e6:.1f} MB one set {one * 1e3:.1f} us "
-            f"({gbs(one) / PEAK_HBM_GBS:.3f}), streaming {st * 1e3:.1f} us ({gbs(st) / PEAK_HBM_GBS:.3f})")
+        entry = {"bytes": nbytes, "streaming_input_sets": n, "policies": {}}
+        for policy, pname in enumerate(STREAM_POLICIES):
+            one = time_op(torch, launcher(*s0, policy))["avg_ms"]
+            st = time_streaming(torch, [launcher(*st_, policy) for st_ in sets])
+            entry["policies"][pname] = {"one_set_us": one * 1e3, "streaming_us": st * 1e3}
+            log(f"[bench] hbm ceiling: {name} {pname} {nbytes / 1e6:.1f} MB one set {one * 1e3:.1f} us "
+                f"({gbs(one) / PEAK_HBM_GBS:.3f}), streaming {st * 1e3:.1f} us ({gbs(st) / PEAK_HBM_GBS:.3f})")
+        del sets, s0, x, b, full, half
+        one = min(v["one_set_us"] for v in entry["policies"].values()) * 1e-3
+        st = min(v["streaming_us"] for v in entry["policies"].values()) * 1e-3
+        entry.update({"one_set_us": one * 1e3, "one_set_GBps": gbs(one), "one_set_frac_of_hbm_peak": gbs(one) / PEAK_HBM_GBS,
+                      "streaming_us": st * 1e3, "streaming_GBps": gbs(st),
+                      "streaming_frac_of_hbm_peak": gbs(st) / PEAK_HBM_GBS})
+        res[name] = entry
     return res
 
 
