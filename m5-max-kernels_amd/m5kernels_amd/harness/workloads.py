@@ -41,14 +41,17 @@ H3_CONFIG = dict(hidden_size=5376, num_attention_heads=56, attention_head_dim=12
 
 
 def load(name):
-    """Suite document from a JSON path, a shipped suite name, or "h3" (generated from
-    H3_CONFIG); case ids must be unique."""
+    """Suite document from a JSON path, a shipped suite name, "h3" or "h3-fused" (both generated
+    from H3_CONFIG); case ids must be unique."""
     p = Path(name)
     if not p.exists():
         p = SUITES / f"{name}.json"
     if not p.exists() and name == "h3":
         data = dict(schema_version=1, description="H3 projection GEMMs and row ops at 128/1024/4096 tokens",
                     cases=h3_cases(H3_CONFIG))
+    elif not p.exists() and name == "h3-fused":
+        data = dict(schema_version=1, description="H3 fused activation-preparation projections at 128/4096/9914 tokens",
+                    cases=h3_fused_cases(H3_CONFIG))
     else:
         data = json.loads(p.read_text())
     cases = [validate(c) for c in data["cases"]]
@@ -84,4 +87,39 @@ def h3_cases(config, tokens=(128, 1024, 4096)):
     for name, k, n in [("adaln", h // 2, 18 * h), ("final_adaln", h // 2, 2 * h), ("time_in", 256, h),
                        ("time_out", h, h // 2)]:
         cases.append(dict(id=f"h3.{name}", op="gemm", m=1, k=k, n=n, component=name))
+    return cases
+
+
+def h3_fused_cases(config, tokens=(128, 4096, 9914)):
+    """The fused projections of the H3 transformer at each token count, with the case ids and
+    options of the reference's fused suites (workloads/h3-norm-hadamard.json,
+    h3-gated-norm-hadamard.json, h3-shift-split.json, rms-quant.json, h3-gate-epilogue.json,
+    h3-qk-rope.json): the norm + H256 + INT8 projections to Q and FFN-up, their residual-gated
+    form, the FP32-rounding norm projection to Q (shift-split), the RMS-quantized Q projection
+    (identity gamma, random gamma, random gamma with H256), the gate-epilogue chains
+    attention -> FFN-up and FFN -> Q, and the Q/K projection with RoPE.  The shift-split and RMS
+    cases are defined at 4096 and 9914 tokens only, as in the reference."""
+    h = config["hidden_size"]
+    d = config["num_attention_heads"] * config["attention_head_dim"]
+    f = config["ffn_dim"]
+    norm = dict(norm="rms", block_size=256, round_output="input")
+    shift = dict(norm="rms", block_size=256, round_output="fp32", threads=256)
+    rms = {"plain": (1, "identity"), "weighted": (1, "random"), "weighted_h256": (256, "random")}
+    cases = []
+    for m in tokens:
+        for name, n in (("q", d), ("ffn_up", f)):
+            cases.append(dict(id=f"h3.norm_{name}.m{m}", op="norm_hadamard_gemm", m=m, n=n, k=h, fusion=dict(norm)))
+            cases.append(dict(id=f"h3.gated_{name}.m{m}", op="gated_norm_hadamard_gemm", m=m, n=n, k=h,
+                              fusion=dict(norm)))
+        if m != 128:
+            cases.append(dict(id=f"h3.shift_q.m{m}", op="norm_hadamard_gemm", m=m, n=d, k=h, fusion=dict(shift)))
+            for name, (block, gamma) in rms.items():
+                cases.append(dict(id=f"rms.{name}.m{m}", op="rms_quant_gemm", m=m, n=d, k=h,
+                                  rms_quant=dict(block_size=block, gamma=gamma, threads=256, epsilon=1e-5)))
+        cases.append(dict(id=f"h3.chain_attention_to_ffn.m{m}", op="gate_epilogue_chain", m=m, k=h, n=f,
+                          previous_k=d, previous_tile=[128, 64, 4, 8]))
+        cases.append(dict(id=f"h3.chain_ffn_to_q.m{m}", op="gate_epilogue_chain", m=m, k=h, n=d, previous_k=f,
+                          previous_tile=[128, 128, 8, 8]))
+        cases.append(dict(id=f"h3.qk_rope.m{m}", op="qk_rope", m=m, k=h, n=d, head_dim=config["attention_head_dim"],
+                          rope_half=48))
     return cases

@@ -36,6 +36,15 @@ def test_load_suites_and_duplicates(tmp_path):
     assert len(h3) == 55
     down = next(c for c in h3 if c["id"] == "h3.ffn_down.m4096")
     assert (down["m"], down["n"], down["k"]) == (4096, 5376, 14336)
+    fused = {c["id"]: c for c in workloads.load("h3-fused")["cases"]}
+    assert len(fused) == 29
+    assert sum(c["op"] == "rms_quant_gemm" for c in fused.values()) == 6
+    assert "h3.shift_q.m128" not in fused and "rms.plain.m128" not in fused
+    chain = fused["h3.chain_attention_to_ffn.m4096"]
+    assert (chain["k"], chain["n"], chain["previous_k"], chain["previous_tile"]) == (5376, 14336, 7168, [128, 64, 4, 8])
+    assert fused["h3.shift_q.m9914"]["fusion"] == dict(norm="rms", block_size=256, round_output="fp32", threads=256)
+    assert fused["rms.weighted_h256.m4096"]["rms_quant"]["block_size"] == 256
+    assert (fused["h3.qk_rope.m9914"]["n"], fused["h3.qk_rope.m9914"]["rope_half"]) == (7168, 48)
     p = tmp_path / "dup.json"
     p.write_text(json.dumps({"cases": [{"id": "x", "op": "gemm", "m": 1, "n": 1, "k": 1}] * 2}))
     with pytest.raises(ValueError, match="duplicate"):
