@@ -12,15 +12,18 @@
 //
 // MFMA blocks.  INT8, BF16 and FP16 use 16 x 16 blocks that take 64 bytes of K per
 // instruction (v_mfma_i32_16x16x64_i8, v_mfma_f32_16x16x32_{bf16,f16}): 8 x 4 blocks per
-// wave, 4 accumulator registers each.  FP8 (v_mfma_scale_f32_32x32x64_f8f6f4) and FP32
-// (v_mfma_f32_32x32x2_f32) use 32 x 32 blocks: 4 x 2 per wave, 16 registers each.  The
-// 16 x 16 form measured ~5% faster than 32 x 32 on the FFN-down and 4096^3 shapes with the
-// same LDS traffic and MFMA cycles per slab.
+// wave, 4 accumulator registers each.  FP8 uses 16 x 16 blocks that take the whole 128-byte
+// stage per instruction (v_mfma_scale_f32_16x16x128_f8f6f4).  FP32 (v_mfma_f32_32x32x2_f32)
+// uses 32 x 32 blocks: 4 x 2 per wave, 16 registers each.  The 16 x 16 form measured ~5%
+// faster than 32 x 32 on the FFN-down and 4096^3 shapes with the same LDS traffic and MFMA
+// cycles per slab (INT8); for FP8, 16 x 16 x 128 with its own stage schedule (see
+// mainloop_dma) measured 5-7% faster than 32 x 32 x 64 on five shapes, with the same bits.
 //
 // Operand layout.  16 x 16: lane l supplies row (l & 15) and the 16-byte K chunk (l >> 4)
-// of a 64-byte sub-step.  32 x 32: row (l & 31) and chunk 2s + (l >> 5) of 32-byte sub-step s
-// (FP32 issues one K = 2 MFMA per float of the chunk), or chunks 2(l >> 5), +1 of a 64-byte
-// sub-step (FP8).  A and B use the same K-slice mapping, so the products pair up correctly
+// of a 64-byte sub-step, or for FP8 the chunks (l >> 4) and 4 + (l >> 4) of the 128-byte
+// stage (32 bytes).  32 x 32 (FP32): row (l & 31) and chunk 2s + (l >> 5) of 32-byte
+// sub-step s, one K = 2 MFMA per float of the chunk.  A and B use the same K-slice mapping,
+// so the products pair up correctly
 // whatever order the hardware sums them in (exact for INT32 accumulation).  Accumulator
 // register r of lane l holds C[(l >> 4) * 4 + r][l & 15] (16 x 16) or
 // C[(r >> 2) * 8 + (l >> 5) * 4 + (r & 3)][l & 31] (32 x 32).
@@ -98,10 +101,10 @@ struct Traits<F32> {
 };
 template <>
 struct Traits<F8> {
-  using acc_t = v16f;
-  static constexpr int MD = 32;
+  using acc_t = v4f;
+  static constexpr int MD = 16;
   static constexpr int elem_bytes = 1;
-  static constexpr int sub_steps = BKB / 64;  // 64 K-bytes per MFMA
+  static constexpr int sub_steps = BKB / 128;  // 128 K-bytes per 16x16x128 MFMA: one per stage
 };
 
 // Operand fragment for one MFMA: 16 bytes (I8/BF16/F16) or 32 bytes (F8).
@@ -133,7 +136,7 @@ __device__ __forceinline__ void mfma(typename Traits<MODE>::acc_t& acc, const Fr
     const v8i bv = {b.lo[0], b.lo[1], b.lo[2], b.lo[3], b.hi[0], b.hi[1], b.hi[2], b.hi[3]};
     // Format codes 0/0 = FP8 E4M3 (OCP) for both operands; zero scales select the
     // unscaled instruction.
-    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, acc, 0, 0, 0, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, 0, 0, 0, 0, 0, 0);
   }
 }
 
@@ -265,17 +268,16 @@ struct FragSet {
 };
 
 // Fragments of sub-step s.  16 x 16 blocks: lane l reads row (l & 15) of each block at
-// logical chunk 4s + (l >> 4) (64-byte sub-steps).  FP8: row (l & 31), chunks 4s + 2(l >> 5)
-// and the next one (64-byte sub-steps, 32 bytes a lane).  FP32: row (l & 31), chunk
-// 2s + (l >> 5) (32-byte sub-steps).  `fq` is the lane's chunk term (l >> 4, 2(l >> 5) or
-// l >> 5), `fsw` the swizzle of its row, which a block offset of 16 or 32 rows leaves alone.
+// logical chunk 4s + (l >> 4) (64-byte sub-steps).  FP8: row (l & 15), chunks (l >> 4) and
+// 4 + (l >> 4) (one 128-byte sub-step, 32 bytes a lane).  FP32: row (l & 31), chunk
+// 2s + (l >> 5) (32-byte sub-steps).  `fq` is the lane's chunk term (l >> 4 or l >> 5), `fsw`
+// the swizzle of its row, which a block offset of 16 or 32 rows leaves alone.
 template <int MODE, class G>
 __device__ __forceinline__ void read_frags(const uint8_t* sa, const uint8_t* sb, int s, int a_row0, int b_row0,
                                            int fq, int fsw, FragSet<MODE, G>& f) {
   constexpr int MD = Blk<MODE, G>::MD;
   if constexpr (MODE == F8) {
-    const int c0 = 4 * s + fq;
-    const int o0 = (c0 ^ fsw) << 4, o1 = ((c0 + 1) ^ fsw) << 4;
+    const int o0 = (fq ^ fsw) << 4, o1 = ((4 + fq) ^ fsw) << 4;
 #pragma unroll
     for (int i = 0; i < Blk<MODE, G>::FM; ++i) {
       const uint8_t* p = sa + (a_row0 + MD * i) * BKB;
@@ -327,7 +329,7 @@ __device__ __forceinline__ void frag_lane(int lane, int& frow, int& fq, int& fsw
     fq = lane >> 4;
   } else {
     frow = lane & 31;
-    fq = MODE == F8 ? 2 * (lane >> 5) : lane >> 5;
+    fq = lane >> 5;
   }
   fsw = swz(frow);
 }
@@ -336,9 +338,8 @@ __device__ __forceinline__ void frag_lane(int lane, int& frow, int& fq, int& fsw
 template <int MODE>
 __device__ __forceinline__ void read_frag(const uint8_t* row, int s, int fq, int fsw, Frag<MODE>& f) {
   if constexpr (MODE == F8) {
-    const int c0 = 4 * s + fq;
-    f.lo = *reinterpret_cast<const v4i*>(row + ((c0 ^ fsw) << 4));
-    f.hi = *reinterpret_cast<const v4i*>(row + (((c0 + 1) ^ fsw) << 4));
+    f.lo = *reinterpret_cast<const v4i*>(row + ((fq ^ fsw) << 4));
+    f.hi = *reinterpret_cast<const v4i*>(row + (((4 + fq) ^ fsw) << 4));
   } else {
     f.lo = *reinterpret_cast<const v4i*>(row + ((((MODE == F32 ? 2 : 4) * s + fq) ^ fsw) << 4));
   }
@@ -349,8 +350,7 @@ __device__ __forceinline__ void read_frag(const uint8_t* row, int s, int fq, int
 // rows, and hook(k) called before row k's reads (the stage DMA uses it).  Scheduling fences keep
 // each read ahead of the MFMA row it is placed before; left alone, the compiler sinks every read
 // next to its first use, which exposes the LDS latency.  Measured on the 16 x 16 modes: INT8
-// +1-4%, BF16 +2-4%; FP8 (two reads per fragment, 253 VGPRs) ran 0-4% slower this way and keeps
-// the compiler's order.
+// +1-4%, BF16 +2-4%.  (FP8, one sub-step per stage, has its own schedule in mainloop_dma.)
 template <int MODE, class G, int I0, int I1, class H>
 __device__ __forceinline__ void mfma_rows_reading(AccTile<MODE, G>& acc, const FragSet<MODE, G>& fc,
                                                   FragSet<MODE, G>& fn, const uint8_t* sa, const uint8_t* sb,
@@ -393,8 +393,9 @@ __host__ __device__ constexpr int64_t k_stages(int64_t Kb) { return (Kb + BKB - 
 // The barrier thus sits between sub-steps: the next stage's first fragments and the DMA have a
 // whole sub-step of MFMAs to hide behind.  Against a barrier after half of the last sub-step's
 // rows (its reads and DMA over the other half), this measured 1.4-1.6% faster at K = 16384 and
-// at FFN-up (N = 16384, K = 4096), equal at 4096^3, same bits.  The 32 x 32 modes (FP8, FP32)
-// keep the barrier after half of the last sub-step, with the DMA in one burst.
+// at FFN-up (N = 16384, K = 4096), equal at 4096^3, same bits.  FP32 (32 x 32 blocks) keeps
+// the barrier after half of the last sub-step, with the DMA in one burst.  FP8 (one sub-step
+// per stage) has the schedule described at stage_f8 below.
 // Stage kt+1's loads have one whole stage to land.  Each accumulator sees K in order, sub-step
 // by sub-step.
 //
@@ -405,7 +406,7 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
                                              int N, int64_t Kb, int tile_m0, int tile_n0, AccTile<MODE, G>& acc,
                                              int64_t kt_begin, int64_t kt_count) {
   constexpr int SUB = Traits<MODE>::sub_steps;
-  static_assert(SUB % 2 == 0, "the last sub-step of a stage uses the second fragment set");
+  static_assert(MODE == F8 || SUB % 2 == 0, "the last sub-step of a stage uses the second fragment set");
   static_assert(!PIPELINED || Traits<MODE>::MD == 16, "interleaved reads are measured for 16 x 16 modes");
   constexpr int FM = Blk<MODE, G>::FM;
   const int tid = threadIdx.x;
@@ -512,9 +513,8 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
       mfma_rows_reading<MODE, G, 0, FM>(acc, f1, f0, stage_a<NXT>(), stage_b<NXT>(), 0, a_row0, b_row0, fq, fsw,
                                         hook);
     } else {
-      // FP8 / FP32 (32 x 32 blocks, two rows per half): half of the last sub-step's rows before the
-      // barrier, and the DMA in one burst (spread over their rows, the DMA state pushed the FP8
-      // kernels past 256 VGPRs).
+      // FP32 (32 x 32 blocks, two rows per half): half of the last sub-step's rows before the
+      // barrier, and the DMA in one burst.
       mfma_rows<MODE, G, 0, FM / 2>(acc, f1);
       wait_stage<0>();
       __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -524,6 +524,89 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
       mfma_rows<MODE, G, FM / 2, FM>(acc, f1);
     }
   };
+  // FP8: one 16 x 16 x 128 MFMA per block and stage (32-byte fragments: chunks fq and 4 + fq),
+  // so there is no second sub-step to read ahead into, and two full fragment sets do not fit
+  // beside the accumulators.  One set of B fragments and a ring of four A fragments (slot i % 4
+  // for block row i).  Per stage (FM = 8):
+  //   rows 0, 1 column by column (B fragment 0 first), reading A rows 2, 3;
+  //   rows 2 .. 4 in order, reading A rows 4 .. 7 (three rows ahead), so the stage's last read
+  //   of this buffer precedes row 4's MFMAs;
+  //   wait for own stage kt+1 loads and all LDS reads; barrier;
+  //   row 5, then rows 6, 7 column by column, with the DMA of stage kt+2 spread over these five
+  //   steps; the next stage's A rows 0, 1 are read around row 5, and each B fragment is re-read
+  //   from the next stage's buffer as soon as its column of row 7 has issued (the next stage's
+  //   first columns cover those reads).
+  // With FM = 4 (the 256 x 128 half tile) there are no middle rows: rows 0, 1, the barrier, then
+  // rows 2, 3 column by column.  Against the 32 x 32 x 64 form (two 64-byte sub-steps, both
+  // fragment sets, barrier after half of the last sub-step) this measured 5-7% faster on the
+  // FFN-down, FFN-up, 4096^3, 9914 x 4096^2 and 4096 x 14336 x 5376 shapes, with the same bits;
+  // a variant reading A two rows ahead (barrier before rows 6, 7) gained 0-2.5%.
+  const uint32_t f8_a0 = static_cast<uint32_t>(a_row0 * BKB + ((fq ^ fsw) << 4));
+  const uint32_t f8_a1 = static_cast<uint32_t>(a_row0 * BKB + (((4 + fq) ^ fsw) << 4));
+  const uint32_t f8_b0 = static_cast<uint32_t>(b_row0 * BKB + ((fq ^ fsw) << 4));
+  const uint32_t f8_b1 = static_cast<uint32_t>(b_row0 * BKB + (((4 + fq) ^ fsw) << 4));
+  auto f8_read = [&](const uint8_t* buf, uint32_t o0, uint32_t o1, int blk, Frag<MODE>& fr) {
+    fr.lo = *reinterpret_cast<const v4i*>(buf + o0 + blk * Blk<MODE, G>::MD * BKB);
+    fr.hi = *reinterpret_cast<const v4i*>(buf + o1 + blk * Blk<MODE, G>::MD * BKB);
+  };
+  Frag<MODE> f8_b[Blk<MODE, G>::FN];
+  Frag<MODE> f8_ring[4];
+  auto stage_f8 = [&](auto cur_tag, int64_t kt) {
+    constexpr int CUR = decltype(cur_tag)::value, NXT = CUR ^ 1;
+    constexpr int FN = Blk<MODE, G>::FN;
+    static_assert(FM % 4 == 0, "ring slots repeat every stage");
+    const uint8_t* ca = stage_a<CUR>();
+    f8_read(ca, f8_a0, f8_a1, 2, f8_ring[2]);
+    f8_read(ca, f8_a0, f8_a1, 3, f8_ring[3]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      mfma<MODE>(acc[0][j], f8_ring[0], f8_b[j]);
+      mfma<MODE>(acc[1][j], f8_ring[1], f8_b[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Rows 2 .. FM - 4 read A three rows ahead (row 2 also reads row 4's), so the last A read of
+    // the stage precedes row FM - 4's MFMAs and the barrier can follow them.
+#pragma unroll
+    for (int i = 2; i < FM - 3; ++i) {
+      if (i == 2 && FM > 4) f8_read(ca, f8_a0, f8_a1, 4, f8_ring[0]);
+      if (i + 3 < FM) f8_read(ca, f8_a0, f8_a1, i + 3, f8_ring[(i + 3) % 4]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) mfma<MODE>(acc[i][j], f8_ring[i % 4], f8_b[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_stage<0>();
+    // The DMA below overwrites this buffer: every wave's reads of it must have returned.
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stage_barrier();
+    const uint8_t* na = stage_a<NXT>();
+    const uint8_t* nb = stage_b<NXT>();
+    // With more than four block rows, row FM - 3 runs after the barrier (in order); then the last
+    // two rows column by column.
+    constexpr int MIDDLE = FM > 4 ? 1 : 0, STEPS = FN + MIDDLE;
+    if constexpr (MIDDLE) {
+      dma_range(stage_a<CUR>(), stage_b<CUR>(), kt + 2, 0, NQ / STEPS);
+      f8_read(na, f8_a0, f8_a1, 0, f8_ring[0]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) mfma<MODE>(acc[FM - 3][j], f8_ring[(FM - 3) % 4], f8_b[j]);
+      __builtin_amdgcn_sched_barrier(0);
+      f8_read(na, f8_a0, f8_a1, 1, f8_ring[1]);
+    } else {
+      f8_read(na, f8_a0, f8_a1, 0, f8_ring[0]);
+      f8_read(na, f8_a0, f8_a1, 1, f8_ring[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      dma_range(stage_a<CUR>(), stage_b<CUR>(), kt + 2, (j + MIDDLE) * NQ / STEPS, (j + MIDDLE + 1) * NQ / STEPS);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma<MODE>(acc[FM - 2][j], f8_ring[(FM - 2) % 4], f8_b[j]);
+      mfma<MODE>(acc[FM - 1][j], f8_ring[(FM - 1) % 4], f8_b[j]);
+      __builtin_amdgcn_sched_barrier(0);
+      f8_read(nb, f8_b0, f8_b1, j, f8_b[j]);
+    }
+  };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
@@ -531,11 +614,23 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   dma(stage_a<1>(), stage_b<1>(), 1);
   wait_stage<G::DMA_INSTR + G::DMA_INSTR_B>();  // stage 0 landed (own loads)
   stage_barrier();
-  read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fq, fsw, f0);
+  if constexpr (MODE == F8) {
+#pragma unroll
+    for (int j = 0; j < Blk<MODE, G>::FN; ++j) f8_read(stage_b<0>(), f8_b0, f8_b1, j, f8_b[j]);
+    f8_read(stage_a<0>(), f8_a0, f8_a1, 0, f8_ring[0]);
+    f8_read(stage_a<0>(), f8_a0, f8_a1, 1, f8_ring[1]);
+  } else {
+    read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fq, fsw, f0);
+  }
   const int64_t kt_padded = (kt_count + 1) / 2 * 2;
   for (int64_t kt = 0; kt < kt_padded; kt += 2) {
-    stage(I0{}, kt);
-    stage(I1{}, kt + 1);
+    if constexpr (MODE == F8) {
+      stage_f8(I0{}, kt);
+      stage_f8(I1{}, kt + 1);
+    } else {
+      stage(I0{}, kt);
+      stage(I1{}, kt + 1);
+    }
   }
   // Drain the trailing (zero) DMAs before the LDS is reused or the wave exits.
   wait_stage<0>();

@@ -406,8 +406,11 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
   q.coalesced = n % 8 == 0 && aligned16(p.c) && (p.residual == nullptr || (aligned16(p.residual) && aligned16(p.gate)));
   if (aligned) {
     int64_t full = -1;
-    const int sched = plan_schedule(Traits<MODE>::MD == 16, MODE == I8, m, n, device_cus(), full);
-    if constexpr (Traits<MODE>::MD == 16) {
+    // The narrow 256 x 224 tile serves the 16 x 16 modes with 16-byte fragments (INT8, BF16,
+    // FP16); FP8's 32-byte fragments for its seven B blocks do not fit beside the accumulators.
+    constexpr bool narrow_ok = Traits<MODE>::MD == 16 && MODE != F8;
+    const int sched = plan_schedule(narrow_ok, MODE == I8, m, n, device_cus(), full);
+    if constexpr (narrow_ok) {
       if (sched == SCHED_NARROW) {
         using G = Grid8Narrow;
         const int64_t wgs = ((m + BM - 1) / BM) * ((n + G::TN - 1) / G::TN);
