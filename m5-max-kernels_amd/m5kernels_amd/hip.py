@@ -348,7 +348,9 @@ def gemm(
         elif aligned and getattr(_override, "schedule", None) is not None:
             splits = 1  # a forced schedule runs unsplit, without the tail split
         elif aligned:
-            env = tuple(os.environ.get(v) for v in ("M5K_GEMM_MIXED_TILES", "M5K_GEMM_NARROW_TILES", "M5K_GEMM_SCHEDULE"))
+            environ = os.environ
+            env = (environ.get("M5K_GEMM_MIXED_TILES"), environ.get("M5K_GEMM_NARROW_TILES"),
+                   environ.get("M5K_GEMM_SCHEDULE"))
             splits, tail = _i8_schedule(m, n, k, _cu_count(a.device), env)
         if tail is not None:
             # Whole tile rows in full rounds, then the remaining rows split along K.  Every

@@ -533,3 +533,28 @@ def test_schedules_random_shapes_bit_identical(monkeypatch, device):
         view = torch.int16 if auto.element_size() == 2 else torch.int32
         assert torch.equal(auto.view(view), plain.view(view)), (m, n, k, mode, sched)
         del a, b, auto, plain
+
+
+def test_ops_launch_on_the_current_stream(device):
+    """The wrappers launch on torch's current stream of the operand's device: on a side stream
+    the handle passed to the library is that stream's, and the results equal the default
+    stream's bit for bit."""
+    from m5kernels_amd import _lib
+
+    g = torch.Generator(device="cpu").manual_seed(7)
+    x = torch.randn((300, 512), generator=g).to(torch.bfloat16).to(device)
+    w = torch.randn((260, 512), generator=g).to(torch.bfloat16).to(device)
+    assert _lib.stream_of(x) == torch.cuda.current_stream(device).cuda_stream
+    wq, ws = quantize(w, "int8")
+    q0, s0 = quantize(x, "int8")
+    y0 = gemm(q0, wq, "int8", a_scales=s0, b_scales=ws, output_dtype=torch.bfloat16)
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        assert _lib.stream_of(x) == side.cuda_stream
+        q1, s1 = quantize(x, "int8")
+        y1 = gemm(q1, wq, "int8", a_scales=s1, b_scales=ws, output_dtype=torch.bfloat16)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+    assert torch.equal(q1, q0) and torch.equal(s1, s0)
+    assert np.array_equal(bits_of(y1), bits_of(y0))

@@ -362,7 +362,7 @@ def test_prep_mixed_table_dtypes_one_dispatch_bit_exact(norm, tables, dtype, bra
                                                             gate_row_map=gmap, row_map=row_map)
     name, args = calls[-1]
     assert name == "m5k_norm_hadamard_quantize"
-    handed = {args[i].value for i in (0, 4, 6, 8, 9, 10)}
+    handed = {args[i] for i in (0, 4, 6, 8, 9, 10)}
     assert handed == {t.data_ptr() for t in (rt, bt, gate, gamma, scale, shift)}
     assert args[5] == _lib.dtype_code(bt)
     oq, os_, orn = _oracle_prep(rt, gamma, scale, shift, signs, 256, norm=norm, branch=bt, gate=gate,
