@@ -111,7 +111,7 @@ def device_tensor(t: torch.Tensor, name: str) -> torch.Tensor:
     """Contiguous view of a ROCm device tensor (copies strided inputs, never mutates)."""
     if not isinstance(t, torch.Tensor):
         raise ValueError(f"{name} must be a torch.Tensor")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"{name} must be a ROCm device tensor (got {t.device}); there is no CPU path")
     return t.contiguous()
 
