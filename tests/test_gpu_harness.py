@@ -153,3 +153,16 @@ def test_every_smoke_case_has_a_passing_backend():
             backend = "norm-shift-split"
         tile = (32, 128, 4, 1) if c["op"] == "qk_rope" else (64, 64, 4, 1)
         _ok(run_case(c, backend, precision, warmup=1, repeat=3, tile=tile))
+
+
+def test_generated_h3_fused_suite_at_128_tokens():
+    """Every case of the generated h3-fused suite at M = 128 (the reference's fused workload
+    files at their smallest token count) passes its gates on its fused backend."""
+    backends = {"norm_hadamard_gemm": "norm-fused", "gated_norm_hadamard_gemm": "residual-fused",
+                "gate_epilogue_chain": "gate-in-gemm", "qk_rope": "qk-fused"}
+    cases = [c for c in workloads.load("h3-fused")["cases"] if c["m"] == 128]
+    assert {c["op"] for c in cases} == set(backends)
+    for c in cases:
+        print(f"case {c['id']}", flush=True)
+        tile = (32, 128, 4, 1) if c["op"] == "qk_rope" else (64, 64, 4, 1)
+        _ok(run_case(c, backends[c["op"]], "int8", warmup=1, repeat=3, tile=tile))
