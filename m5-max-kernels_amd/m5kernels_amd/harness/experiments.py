@@ -39,6 +39,7 @@ from .. import (
     quantize,
     rms_quantize,
     rotate,
+    rotate_quantize,
     shift_split_condition,
     unfused_norm,
 )
@@ -761,7 +762,8 @@ def prepare_gate_epilogue_chain(c, backend, precision, seed, distribution, tile)
     ri, ci, wi0 = nx.sample_indices(m), nx.sample_indices(n), nx.sample_indices(h)
 
     def input_prepare():
-        return quantize(rotate(x, block, signs0), "int8", tag="chain_online")
+        # One dispatch, the same codes and scales as quantize(rotate(x)).
+        return rotate_quantize(x, block, signs0)
 
     rotated_x = rotate(x, block, signs0)
     rotated_w0, rotated_w1 = rotate(w0, block, signs0), rotate(w1, block, signs1)
@@ -867,7 +869,7 @@ def prepare_gate_epilogue_chain(c, backend, precision, seed, distribution, tile)
         residual_rounding="BF16(R + float32(BF16(branch))*float32(gate)); no BF16 product round",
         normalization_rounding="completed AdaLN to BF16 before H256",
         returned_outputs=["next projection", "updated residual"],
-        preceding_input_preparation="online H256 and INT8 packing",
+        preceding_input_preparation="online H256 and INT8 packing in one dispatch (the codes and scales of quantize(rotate(x)))",
         main_timing_scope="both projections and transition, resident preceding INT8 activation",
         previous_tile=list(previous_tile),
         next_tile=list(tile),
@@ -980,7 +982,9 @@ def prepare_qk_rope(c, backend, precision, seed, distribution, tile):
         return _f64(output.index_select(0, _idx(heads)).index_select(1, _idx(rows))).reshape(-1)
 
     def activation_prepare():
-        return quantize(rotate(x, block, signs), "int8", tag="qk_online")
+        # The online H + INT8 in one dispatch: the same codes and scales as the reference's
+        # quantize(rotate(x)), whose two halves the stages below still time one by one.
+        return rotate_quantize(x, block, signs)
 
     rotated_a, rotated_w = rotate(x, block, signs), rotate(w, block, signs)
     aq, sa = quantize(rotated_a, "int8", tag="qk_online")
@@ -1043,6 +1047,7 @@ def prepare_qk_rope(c, backend, precision, seed, distribution, tile):
         and a_code_diff <= 1 and w_code_diff <= 1
     )
     meta = dict(
+        online_activation_preparation="block Hadamard and INT8 in one dispatch (the codes and scales of quantize(rotate(x)))",
         compute_path=backend,
         operation_scope="one Q or K projection, not grouped QKV or attention",
         input_dtype="bf16",
