@@ -207,6 +207,10 @@ def _prepare_hadamard_gemm(c, x, w, ri, ci, original, precision, tile):
         return gemm(q, bq, precision, tile, a_scales=scale, b_scales=sb, output_dtype=BF)
 
     def online_prepare():
+        # INT8: the rotation and quantizer in one dispatch (the codes and scales of
+        # quantize(rotate(x))); FP8 keeps the two.  The stages above time the halves one by one.
+        if precision == "int8":
+            return rotate_quantize(x, block, signs)
         return quantize(rotation(x), precision, tag="hadamard_online")
 
     stages = {
@@ -217,6 +221,9 @@ def _prepare_hadamard_gemm(c, x, w, ri, ci, original, precision, tile):
     }
     meta = dict(
         compute_path="block_hadamard_then_mfma_" + precision,
+        online_activation_preparation=("block Hadamard and INT8 in one dispatch (the codes and scales of "
+                                       "quantize(rotate(x)))" if precision == "int8" else
+                                       "block Hadamard, then the FP8 quantizer"),
         input_dtype=_dtype_name(x),
         rotated_dtype="float32",
         output_dtype="bfloat16",
