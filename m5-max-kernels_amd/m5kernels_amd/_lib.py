@@ -8,6 +8,9 @@ library is missing or a tensor is not on a ROCm device, the call raises.
 from __future__ import annotations
 
 import ctypes
+import functools
+import re
+from numbers import Integral, Real
 from pathlib import Path
 
 import torch
@@ -98,6 +101,26 @@ def call(name: str, *args) -> None:
     rc = getattr(lib, name)(*args)
     if rc != 0:
         raise RuntimeError(f"{name} failed ({rc}): {lib.m5k_last_error().decode(errors='replace')}")
+
+
+def is_int(v) -> bool:
+    """An integer that is not a bool (numbers.Integral), with plain int checked first."""
+    return type(v) is int or (not isinstance(v, bool) and isinstance(v, Integral))
+
+
+def is_real(v) -> bool:
+    """A real number that is not a bool (numbers.Real), with plain float and int checked first."""
+    return type(v) is float or type(v) is int or (not isinstance(v, bool) and isinstance(v, Real))
+
+
+@functools.lru_cache(maxsize=256)
+def _identifier(tag: str) -> bool:
+    return re.fullmatch(r"[A-Za-z_][A-Za-z_0-9]*", tag) is not None
+
+
+def is_identifier(tag) -> bool:
+    """A nonempty string of identifier characters (the reference's kernel-name tag rule)."""
+    return isinstance(tag, str) and _identifier(tag)
 
 
 def dtype_code(t: torch.Tensor) -> int:

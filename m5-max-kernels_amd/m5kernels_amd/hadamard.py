@@ -12,7 +12,6 @@ reference's switch and default: "metal" (the default; alias "hip") selects the g
 
 from __future__ import annotations
 
-from numbers import Integral
 
 import torch
 
@@ -23,7 +22,7 @@ _FLOAT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
 def _validate(x, block_size, signs):
-    if isinstance(block_size, bool) or not isinstance(block_size, Integral) or block_size <= 0 or block_size & (
+    if not _lib.is_int(block_size) or block_size <= 0 or block_size & (
         block_size - 1
     ):
         raise ValueError("block_size must be a positive integer power of two")

@@ -22,8 +22,6 @@ Platform notes (contract unchanged):
 from __future__ import annotations
 
 import math
-import re
-from numbers import Integral, Real
 
 import torch
 
@@ -54,13 +52,13 @@ def _validate_common(x, gamma, scale, shift, norm, epsilon, round_output, thread
         norm = "layer"
     if norm not in ("rms", "layer"):
         raise ValueError("norm must be 'rms' or 'layer'")
-    if isinstance(epsilon, bool) or not isinstance(epsilon, Real):
+    if not _lib.is_real(epsilon):
         raise ValueError("epsilon must be a positive finite real scalar")
     if not math.isfinite(epsilon) or epsilon <= 0:
         raise ValueError("epsilon must be a positive finite real scalar")
     if round_output not in ("input", "fp32"):
         raise ValueError("round_output must be 'input' or 'fp32'")
-    if isinstance(threads, bool) or not isinstance(threads, Integral):
+    if not _lib.is_int(threads):
         raise ValueError("threads must be an integer")
     if threads not in (128, 256):
         raise NotImplementedError("supported threadgroup sizes are 128 and 256")
@@ -68,7 +66,7 @@ def _validate_common(x, gamma, scale, shift, norm, epsilon, round_output, thread
 
 
 def _validate_rotation(x, signs, block_size, passes, tag):
-    if isinstance(block_size, bool) or not isinstance(block_size, Integral) or block_size <= 0 or block_size & (
+    if not _lib.is_int(block_size) or block_size <= 0 or block_size & (
         block_size - 1
     ):
         raise ValueError("block_size must be a positive integer power of two")
@@ -80,7 +78,7 @@ def _validate_rotation(x, signs, block_size, passes, tag):
         raise ValueError("signs must be an int8 vector of length K containing only +/-1")
     if passes not in ("one_read", "two_read"):
         raise ValueError("passes must be 'one_read' or 'two_read'")
-    if not isinstance(tag, str) or re.fullmatch(r"[A-Za-z_][A-Za-z_0-9]*", tag) is None:
+    if not _lib.is_identifier(tag):
         raise ValueError("tag must be a valid nonempty Metal identifier")
 
 
@@ -209,11 +207,11 @@ def fused_gated_residual_norm_hadamard_quantize(
 def gated_residual_add(residual, branch, gate, *, gate_row_map=None, threads=256, tag="default"):
     """Staged FP32 gated addition with one residual-dtype cast (norm_hadamard.py:280-300)."""
     _validate_gate(residual, branch, gate, gate_row_map)
-    if isinstance(threads, bool) or not isinstance(threads, Integral):
+    if not _lib.is_int(threads):
         raise ValueError("threads must be an integer")
     if threads not in (128, 256):
         raise NotImplementedError("supported threadgroup sizes are 128 and 256")
-    if not isinstance(tag, str) or re.fullmatch(r"[A-Za-z_][A-Za-z_0-9]*", tag) is None:
+    if not _lib.is_identifier(tag):
         raise ValueError("tag must be a valid nonempty Metal identifier")
     if residual.shape[1] % 8:
         raise NotImplementedError("K must be a multiple of 8 on MI355X")

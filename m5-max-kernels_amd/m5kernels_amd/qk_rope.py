@@ -13,7 +13,6 @@ from __future__ import annotations
 
 import math
 import struct
-from numbers import Integral, Real
 
 import torch
 
@@ -24,7 +23,7 @@ HEAD_DIM = 128
 
 
 def _epsilon(epsilon):
-    if isinstance(epsilon, bool) or not isinstance(epsilon, Real) or not math.isfinite(epsilon) or epsilon <= 0:
+    if not _lib.is_real(epsilon) or not math.isfinite(epsilon) or epsilon <= 0:
         raise ValueError("epsilon must be a positive finite real scalar")
     try:
         value = struct.unpack("=f", struct.pack("=f", float(epsilon)))[0]
@@ -50,7 +49,7 @@ def _validate_norm(m, n, gamma, cos, sin, epsilon):
 def _validate_tile(tile):
     if not isinstance(tile, (tuple, list)) or len(tile) != 4:
         raise ValueError("tile must contain TM, TN, SIMD groups and M swizzle")
-    if any(isinstance(v, bool) or not isinstance(v, Integral) for v in tile):
+    if any(not _lib.is_int(v) for v in tile):
         raise ValueError("tile entries must be integers")
     tm, tn, groups, swizzle = map(int, tile)
     if tm not in (16, 32, 64, 128) or tn not in (64, 128) or groups not in (4, 8):
@@ -134,7 +133,7 @@ def qk_norm_rope(projected, gamma, cos, sin, *, epsilon=1e-5, threads=128):
         raise ValueError("projected must be a bfloat16 [M,N] matrix")
     m, n = projected.shape
     rope_half, epsilon = _validate_norm(m, n, gamma, cos, sin, epsilon)
-    if isinstance(threads, bool) or not isinstance(threads, Integral):
+    if not _lib.is_int(threads):
         raise ValueError("threads must be an integer")
     if threads not in (128, 256):
         raise NotImplementedError("standalone Q/K normalization supports 128 or 256 threads")

@@ -11,9 +11,7 @@ names); the gfx950 kernel always uses one 256-thread workgroup per row.
 from __future__ import annotations
 
 import math
-import re
 import struct
-from numbers import Integral, Real
 
 import torch
 
@@ -36,7 +34,7 @@ def rms_quantize(x, gamma, signs, block_size=1, *, threads=256, fold_scale=True,
         raise ValueError("gamma must be a float32 vector of length K")
     if tuple(signs.shape) != (x.shape[1],) or signs.dtype != torch.int8:
         raise ValueError("signs must be an int8 vector of length K containing only +/-1")
-    if isinstance(block_size, bool) or not isinstance(block_size, Integral) or block_size <= 0 or block_size & (
+    if not _lib.is_int(block_size) or block_size <= 0 or block_size & (
         block_size - 1
     ):
         raise ValueError("block_size must be a positive integer power of two")
@@ -44,13 +42,13 @@ def rms_quantize(x, gamma, signs, block_size=1, *, threads=256, fold_scale=True,
         raise NotImplementedError("supported blocks are 1 and powers of two from 32 through 1024")
     if x.shape[1] % block_size:
         raise NotImplementedError("K must be divisible by block_size; padding is not implicit")
-    if isinstance(threads, bool) or not isinstance(threads, Integral):
+    if not _lib.is_int(threads):
         raise ValueError("threads must be an integer")
     if threads not in (128, 256, 512):
         raise NotImplementedError("supported threadgroup sizes are 128, 256 and 512")
     if not isinstance(fold_scale, bool):
         raise ValueError("fold_scale must be a boolean")
-    if isinstance(epsilon, bool) or not isinstance(epsilon, Real) or not math.isfinite(epsilon) or epsilon <= 0:
+    if not _lib.is_real(epsilon) or not math.isfinite(epsilon) or epsilon <= 0:
         raise ValueError("epsilon must be a positive finite real scalar")
     try:
         epsilon = struct.unpack("=f", struct.pack("=f", float(epsilon)))[0]
@@ -58,7 +56,7 @@ def rms_quantize(x, gamma, signs, block_size=1, *, threads=256, fold_scale=True,
         raise ValueError("epsilon must remain finite and positive in float32") from None
     if not math.isfinite(epsilon) or epsilon <= 0:
         raise ValueError("epsilon must remain finite and positive in float32")
-    if not isinstance(tag, str) or re.fullmatch(r"[A-Za-z_][A-Za-z_0-9]*", tag) is None:
+    if not _lib.is_identifier(tag):
         raise ValueError("tag must be a valid nonempty Metal identifier")
     m, k = x.shape
     x = _lib.aligned_device_tensor(x, "x")
