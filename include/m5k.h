@@ -203,6 +203,18 @@ int m5k_gemm_f8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_
                 void* stream);
 
 /*
+ * Split-K FP8 linear for short M: the same contract as m5k_gemm_f8 (metal.gemm(a, b, "fp8", ...),
+ * src/m5kernels/metal.py:75-80,191-194), computed as `splits` K ranges per output tile into
+ * FP32 partials workspace[splits][m][n] (workspace_elems >= splits*m*n floats, caller-owned),
+ * summed in split order before the scale epilogue.  Deterministic; its FP32 sums may differ
+ * from m5k_gemm_f8's in the last bits (FP8 accumulation order is not pinned).  splits in
+ * [1, 64]; operands 16-byte aligned.
+ */
+int m5k_gemm_f8_splitk(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                       const float* a_scales, const float* b_scales, void* c, int c_dtype, int splits,
+                       float* workspace, int64_t workspace_elems, void* stream);
+
+/*
  * Floating GEMM with FP32 accumulation.  Replaces metal.gemm(a, b, "bf16"|"fp16", ...)
  * (src/m5kernels/metal.py:59-74,101-107).  a: [m,k], b: [n,k] of ab_dtype (BF16/F16).
  * c = O(acc).  Optional gated residual epilogue as for m5k_gemm_i8 (BF16 only).

@@ -445,12 +445,13 @@ int launch(const void* a, const void* b, int64_t m, int64_t n, int64_t k, const 
 // workgroups, each over a contiguous range of 128-byte K stages, writing raw INT32 partial tiles to
 // workspace[s][M][N]; a second kernel sums the partials in split order (exact: INT32 sums of
 // a bounded dot product) and applies the same FP32 epilogue as gemm_kernel, so the output
-// is bit-identical to the plain launch.
-template <int MODE, class G = KernelGrid>
+// is bit-identical to the plain launch.  P is the partial type: INT32 for INT8, FP32 for the
+// FP8 split (launch_f8_splitk).
+template <int MODE, class G = KernelGrid, class P = int32_t>
 __global__ __launch_bounds__(G::THREADS, 1) void gemm_splitk_kernel(const uint8_t* __restrict__ A,
                                                                     const uint8_t* __restrict__ B, int M, int N,
                                                                     int64_t Kb, int splits, int64_t stages_per_split,
-                                                                    int32_t* __restrict__ partial) {
+                                                                    P* __restrict__ partial) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + G::TN - 1) / G::TN;
   const int tile = static_cast<int>(blockIdx.x) / splits, s = static_cast<int>(blockIdx.x) % splits;
   int tm, tn;
@@ -461,19 +462,19 @@ __global__ __launch_bounds__(G::THREADS, 1) void gemm_splitk_kernel(const uint8_
   const int64_t kt1 = kt0 + stages_per_split < kt_total ? kt0 + stages_per_split : kt_total;
   AccTile<MODE, G> acc;
   mainloop_dma<MODE, G>(A, B, M, N, Kb, m0, n0, acc, kt0, kt1 - kt0);
-  int32_t* out = partial + static_cast<int64_t>(s) * M * N;
+  P* out = partial + static_cast<int64_t>(s) * M * N;
   for_each_acc<G>(acc, m0, n0, [&](int m, int n, auto v) {
     if (m < M && n < N) out[static_cast<int64_t>(m) * N + n] = v;
   });
 }
 
-template <int OUT_DT, int BIAS, int GATE>
-__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ partial, int splits, int M,
-                                                              int N, EpiParams p) {
+template <int OUT_DT, int BIAS, int GATE, class P = int32_t>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const P* __restrict__ partial, int splits, int M, int N,
+                                                              EpiParams p) {
   const int64_t total = static_cast<int64_t>(M) * N;
   for (int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
        idx += static_cast<int64_t>(gridDim.x) * 256) {
-    int32_t v = 0;
+    P v = 0;
     for (int s = 0; s < splits; ++s) v += partial[s * total + idx];
     const int m = static_cast<int>(idx / N), n = static_cast<int>(idx - static_cast<int64_t>(m) * N);
     float value = (static_cast<float>(v) * p.sa[m]) * p.sb[n];
@@ -540,6 +541,35 @@ int launch_i8_splitk(const int8_t* a, const int8_t* b, int64_t m, int64_t n, int
                       : launch_splitk<M5K_BF16, EPI_NONE, EPI_VECTOR>(a, b, m, n, k, p, splits, workspace, st, name);
   }
   return launch_splitk<OUT_DT, EPI_NONE, EPI_NONE>(a, b, m, n, k, p, splits, workspace, st, name);
+}
+
+// FP8 split-K: FP32 partial tiles, summed in split order by the same epilogue kernel.  The
+// 256 x 64 tile's waves hold two 16-row blocks, fewer than FP8's stage schedule takes, so the
+// split tiles are 256 x 128 where their workgroups fit in one round, else 256 x 256.  Each K
+// range is its own FP32 accumulation, so the output can differ from the unsplit launch in the
+// last bits of the FP32 sum (FP8's accumulation order is not pinned); it is deterministic.
+template <int OUT_DT>
+int launch_f8_splitk(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k, const EpiParams& p,
+                     int splits, float* workspace, hipStream_t st, const char* name) {
+  const int64_t kt_total = k_stages(k);
+  const int64_t per = (kt_total + splits - 1) / splits;
+  const int used = static_cast<int>((kt_total + per - 1) / per);  // no empty split
+  const int cus = device_cus();
+  const bool half = cus > 0 && ((m + BM - 1) / BM) * ((n + HalfGrid::TN - 1) / HalfGrid::TN) * used <= cus;
+  const int tn = half ? HalfGrid::TN : BN;
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + tn - 1) / tn);
+  M5K_REQUIRE(tiles * used <= 0x7FFFFFFF, "%s: too many workgroups", name);
+  const dim3 wgs(static_cast<unsigned>(tiles * used)), block(KernelGrid::THREADS);
+  if (half)
+    gemm_splitk_kernel<F8, HalfGrid, float><<<wgs, block, 0, st>>>(a, b, (int)m, (int)n, k, used, per, workspace);
+  else
+    gemm_splitk_kernel<F8, KernelGrid, float><<<wgs, block, 0, st>>>(a, b, (int)m, (int)n, k, used, per, workspace);
+  if (int rc = launch_status(name)) return rc;
+  const int64_t blocks = (m * n + 255) / 256;
+  const unsigned grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+  splitk_epilogue_kernel<OUT_DT, EPI_NONE, EPI_NONE, float>
+      <<<dim3(grid), dim3(256), 0, st>>>(workspace, used, (int)m, (int)n, p);
+  return launch_status(name);
 }
 
 inline int check_shape(int64_t m, int64_t n, int64_t k, const char* name) {

@@ -56,6 +56,7 @@ SIGNATURES = {
     "m5k_gemm_i8_splitk": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _i32, _p, _i64, _p],
     "m5k_gemm_i8_splitk_noalloc": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _i32, _p],
     "m5k_gemm_f8": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _p],
+    "m5k_gemm_f8_splitk": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _p, _i64, _p],
     "m5k_gemm_float": [_p, _p, _i32, _i64, _i64, _i64, _p, _i32, _p, _p, _p, _p],
     "m5k_hadamard_rotate": [_p, _i32, _i64, _i64, _i32, _p, _p, _p],
     "m5k_hadamard_quantize_rows": [_p, _i32, _i64, _i64, _i32, _p, _p, _p, _p],

@@ -92,7 +92,7 @@ def _check_vector(t, n, dtype, message):
         raise ValueError(message)
 
 
-def splitk_plan(m, n, k, cus=256):
+def splitk_plan(m, n, k, cus=256, skinny=True):
     """Number of K ranges per output tile for the W8A8 linear (1 = one workgroup per tile).
 
     Shapes with few 256 x 256 tiles (short M) leave most of the 256 CUs idle; splitting K
@@ -108,12 +108,13 @@ def splitk_plan(m, n, k, cus=256):
     ones, 1.1-1.45x at M 384-1024).  Above M = 768, with at least 32 tiles of 256 x 256, the
     plain launch (the library's mixed or narrow tiles) measured faster than any split (M 1024:
     44.8 against 57.6 us at N = K = 5376, 35.5 against 37.2 us at N = K = 4096), so no split is
-    planned there; narrow outputs (N 32-96) keep the split, their few tiles leaving most CUs idle."""
+    planned there; narrow outputs (N 32-96) keep the split, their few tiles leaving most CUs idle.
+    skinny=False plans without the 256 x 64 tile (the FP8 split, m5k_gemm_f8_splitk)."""
     if m > 768 and -(-m // 256) * -(-n // 256) >= 32:
         return 1
     slabs = -(-k // 64)
     tiles_m = -(-m // 256)
-    for width in ((64, 128) if k <= 8192 else (128,)):
+    for width in ((64, 128) if k <= 8192 and skinny else (128,)):
         splits = min(cus // (tiles_m * -(-n // width)), slabs // 4, max(2, k // (2 * m)), 64)
         if splits >= 2:
             return splits
@@ -222,6 +223,13 @@ def _i8_schedule(m, n, k, cus, env):
     if splits == 1 and launch_plan("int8", m, n, cus)[0] == "plain":
         tail = tail_split_plan(m, n, k, cus)
     return splits, tail
+
+
+@functools.lru_cache(maxsize=4096)
+def _f8_splits(m, n, k, cus, forced):
+    """K ranges per tile of an aligned FP8 linear (1: the plain launch), cached per shape, CU
+    count and M5K_GEMM_SCHEDULE (a schedule forced from the environment runs unsplit)."""
+    return 1 if forced else splitk_plan(m, n, k, cus, skinny=False)
 
 
 def gemm(
@@ -400,6 +408,19 @@ def gemm(
             stream,
         )
     elif mode == "fp8":
+        # Short M: split-K with FP32 partials (deterministic; the FP32 sums may differ from the
+        # unsplit launch's in the last bits, FP8's accumulation order being unpinned).  A
+        # schedule forced for the tuner runs unsplit, as named.
+        splits = 1
+        if a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0 and getattr(_override, "schedule", None) is None:
+            splits = _f8_splits(m, n, k, _cu_count(a.device), os.environ.get("M5K_GEMM_SCHEDULE"))
+        if splits > 1:
+            workspace = torch.empty((splits, m, n), dtype=torch.float32, device=a.device)
+            _lib.call(
+                "m5k_gemm_f8_splitk", _lib.ptr(a), _lib.ptr(b), m, n, k, _lib.ptr(a_scales), _lib.ptr(b_scales),
+                _lib.ptr(c), out_code, splits, _lib.ptr(workspace), workspace.numel(), stream,
+            )
+            return c
         _lib.call(
             "m5k_gemm_f8",
             _lib.ptr(a),

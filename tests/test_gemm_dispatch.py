@@ -34,7 +34,7 @@ def recorder(monkeypatch):
     def call(name, *args):
         if name in HOST_ONLY:
             return real_call(name, *args)
-        splits = args[14] if name.startswith("m5k_gemm_i8_splitk") else None
+        splits = args[14] if name.startswith("m5k_gemm_i8_splitk") else args[9] if name == "m5k_gemm_f8_splitk" else None
         calls.append((name, splits, _thread_schedule()))
 
     monkeypatch.setattr(_lib, "call", call)
@@ -42,6 +42,7 @@ def recorder(monkeypatch):
     monkeypatch.setattr(_lib, "stream_of", lambda t: None)
     monkeypatch.setattr(hip, "_cu_count", lambda device: 256)
     hip._i8_schedule.cache_clear()
+    hip._f8_splits.cache_clear()
     return calls
 
 
@@ -98,3 +99,30 @@ def test_set_schedule_rejects_unknown_codes():
     assert lib.m5k_gemm_set_schedule(4, None) != 0
     assert lib.m5k_gemm_set_schedule(-2, None) != 0
     assert _thread_schedule() == -1
+
+
+def test_fp8_short_m_splits_k_and_large_m_or_forced_plain_does_not(recorder):
+    # h3 ffn_down at M = 128: 21 tiles of 256 x 256 leave most CUs idle, so the FP8 GEMM splits K
+    # over 256 x 128 tiles; at M = 4096, and under a forced schedule, it runs unsplit.
+    m, n, k = 128, 5376, 14336
+    planned = hip.splitk_plan(m, n, k, 256, skinny=False)
+    assert planned > 1 and -(-n // 128) * planned <= 256
+    a, b = torch.zeros((m, k), dtype=torch.uint8), torch.zeros((n, k), dtype=torch.uint8)
+    kw = dict(a_scales=torch.ones(m), b_scales=torch.ones(n), output_dtype=torch.bfloat16)
+    hip.gemm(a, b, "fp8", **kw)
+    assert recorder == [("m5k_gemm_f8_splitk", planned, -1)]
+    recorder.clear()
+    with hip.launch_override("plain"):
+        hip.gemm(a, b, "fp8", **kw)
+    assert recorder == [("m5k_gemm_f8", None, 0)]
+    recorder.clear()
+    big = torch.zeros((4096, k), dtype=torch.uint8)
+    hip.gemm(big, b, "fp8", a_scales=torch.ones(4096), b_scales=torch.ones(n), output_dtype=torch.bfloat16)
+    assert recorder == [("m5k_gemm_f8", None, -1)]
+
+
+def test_fp8_split_plan_never_needs_the_skinny_tile():
+    for m, n, k in [(1, 4096, 4096), (16, 5376, 5376), (128, 7168, 5376), (256, 4096, 16384), (512, 96, 5376)]:
+        s8, s = hip.splitk_plan(m, n, k, 256), hip.splitk_plan(m, n, k, 256, skinny=False)
+        assert 1 <= s <= 64 and (s == 1 or -(-m // 256) * -(-n // 128) * s <= 256 or -(-m // 256) * -(-n // 256) * s <= 224)
+        assert s8 >= 1

@@ -193,7 +193,7 @@ def test_fp8_gemm(shape, schedule, device):
                @ ref.dequantize(np_of(bq), np_of(sb), "fp8").astype(np.float64).T)
     y32 = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb)
     assert y32.dtype == torch.float32
-    # The FP8 MFMA sums its 64 products with less than FP32 precision before adding them
+    # The FP8 MFMA sums its 128 products with less than FP32 precision before adding them
     # to the FP32 accumulator (measured rel-L2 ~1.6e-5 at K=128); the bar is 1e-3.
     assert ref.metrics(np_of(y32), decoded)["relative_l2"] < 1e-4
     y = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb, output_dtype=torch.bfloat16)
@@ -558,3 +558,30 @@ def test_ops_launch_on_the_current_stream(device):
     torch.cuda.synchronize(device)
     assert torch.equal(q1, q0) and torch.equal(s1, s0)
     assert np.array_equal(bits_of(y1), bits_of(y0))
+
+
+@pytest.mark.parametrize("shape", [(128, 5376, 14336), (16, 4096, 4096), (300, 1000, 1024), (1, 96, 5376)])
+def test_fp8_split_k_against_float64_and_unsplit(shape, device):
+    """Short-M FP8 GEMMs take the split-K launch (FP32 partials summed in split order): within the
+    FP8 bar of the decoded float64 product, within FP32 rounding of the unsplit launch, and the
+    same bits on a second call."""
+    from m5kernels_amd import hip
+
+    m, n, k = shape
+    print(f"case m={m} n={n} k={k}", flush=True)
+    assert hip.splitk_plan(m, n, k, 256, skinny=False) > 1
+    g = torch.Generator(device="cpu").manual_seed(m + n + k)
+    a = torch.randn((m, k), generator=g).to(torch.bfloat16).to(device)
+    b = (torch.randn((n, k), generator=g) * 0.02).to(torch.bfloat16).to(device)
+    aq, sa = quantize(a, "fp8")
+    bq, sb = quantize(b, "fp8")
+    decoded = (ref.dequantize(np_of(aq), np_of(sa), "fp8").astype(np.float64)
+               @ ref.dequantize(np_of(bq), np_of(sb), "fp8").astype(np.float64).T)
+    y_split = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb)
+    with hip.launch_override("plain"):
+        y_plain = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb)
+    assert ref.metrics(np_of(y_split), decoded)["relative_l2"] < 1e-4
+    assert ref.metrics(np_of(y_split), np_of(y_plain).astype(np.float64))["relative_l2"] < 1e-5
+    assert torch.equal(gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb), y_split)
+    y16 = gemm(aq, bq, "fp8", a_scales=sa, b_scales=sb, output_dtype=torch.bfloat16)
+    assert ref.metrics(y16.float().cpu().numpy(), decoded)["relative_l2"] < 0.008
