@@ -108,11 +108,20 @@ def splitk_plan(m, n, k, cus=256, skinny=True):
     ones, 1.1-1.45x at M 384-1024).  Above M = 768, with at least 32 tiles of 256 x 256, the
     plain launch (the library's mixed or narrow tiles) measured faster than any split (M 1024:
     44.8 against 57.6 us at N = K = 5376, 35.5 against 37.2 us at N = K = 4096), so no split is
-    planned there; narrow outputs (N 32-96) keep the split, their few tiles leaving most CUs idle.
+    planned there, unless K is long and the tiles fill under 3/8 of the CUs (then the chip takes
+    cus // tiles K ranges); narrow outputs (N 32-96) keep the split, their few tiles leaving most
+    CUs idle.
     skinny=False plans without the 256 x 64 tile (the FP8 split, m5k_gemm_f8_splitk)."""
-    if m > 768 and -(-m // 256) * -(-n // 256) >= 32:
-        return 1
     slabs = -(-k // 64)
+    if m > 768 and -(-m // 256) * -(-n // 256) >= 32:
+        # One partial round that even the mixed launch's half tiles fill to under 3/4, over a
+        # long K: whole-tile K ranges fill the chip instead (M 1024: 84 tiles at N 5376, K 14336
+        # ran 94.0 -> 84.3 us with 3 ranges; 64 at N 4096, K 16384 97.7 -> 77.5 us with 4; at
+        # K 5376, or M 1536 and up, the plain and mixed launches stayed ahead).
+        tiles = -(-m // 256) * -(-n // 256)
+        if k >= 8192 and 2 * tiles <= 3 * cus // 4:
+            return max(2, min(cus // tiles, slabs // 4, 64))
+        return 1
     tiles_m = -(-m // 256)
     for width in ((64, 128) if k <= 8192 and skinny else (128,)):
         splits = min(cus // (tiles_m * -(-n // width)), slabs // 4, max(2, k // (2 * m)), 64)

@@ -277,6 +277,11 @@ def test_tail_split_plan_decisions():
     # except for narrow outputs whose few tiles leave most CUs idle.
     assert splitk_plan(1024, 5376, 5376) == 1 and splitk_plan(1024, 4096, 4096) == 1
     assert splitk_plan(1024, 96, 5376) == 2 and splitk_plan(1024, 32, 5376) == 2
+    # ... and for long K when the tiles fill under 3/8 of the CUs: whole-tile K ranges fill the
+    # chip (M 1024 at N 5376 / 4096 and K 14336 / 16384); M 1536 and up keeps the plain launch.
+    assert splitk_plan(1024, 5376, 14336) == 3 and splitk_plan(1024, 4096, 16384) == 4
+    assert splitk_plan(1536, 5376, 14336) == 1 and splitk_plan(2048, 4096, 16384) == 1
+    assert splitk_plan(1024, 5376, 14336, skinny=False) == 3
     # Two tile rows: 256 x 64 split tiles while 2 * ceil(N / 64) * splits fits one round.
     assert splitk_plan(512, 4096, 4096) == 2 and splitk_plan(512, 1536, 5376) == 5
     # One tile row, K <= 8192: split counts sized to 256 x 64 tiles (64 columns at N 4096).
