@@ -484,6 +484,36 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
         if (kk == k) dma_range(sa, sb, kr, kk * NQ / ROWS, (kk + 1) * NQ / ROWS);
     };
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  const int64_t kt_padded = (kt_count + 1) / 2 * 2;
+
+  // A wave whose block rows all lie past the matrix (short M: rows [M, 256) of the tile) has
+  // nothing to multiply.  It still moves its share of every stage and meets every barrier of the
+  // loop below (prologue, one per stage, drain), at the same points, and leaves its
+  // accumulators at zero, as the zero rows it would load give; the epilogue stores no row past
+  // M.  At M = 128 this halves the tile's MFMAs and fragment reads (one of each SIMD's two waves
+  // idles); the outputs are unchanged.  Eight-wave grids only: the four-wave grid, at 256
+  // accumulators, spills with the second loop beside its main one.
+  if (G::WAVES == 8 && (uwave / G::WAVES_N) * G::WM >= rows_a) {
+    auto idle_stage = [&](auto cur_tag, int64_t kt) {
+      constexpr int CUR = decltype(cur_tag)::value;
+      wait_stage<0>();
+      stage_barrier();
+      dma(stage_a<CUR>(), stage_b<CUR>(), kt + 2);
+    };
+    dma(stage_a<0>(), stage_b<0>(), 0);
+    dma(stage_a<1>(), stage_b<1>(), 1);
+    wait_stage<NQ>();
+    stage_barrier();
+    for (int64_t kt = 0; kt < kt_padded; kt += 2) {
+      idle_stage(I0{}, kt);
+      idle_stage(I1{}, kt + 1);
+    }
+    wait_stage<0>();
+    stage_barrier();
+    return;
+  }
 
   int frow, fq, fsw;
   frag_lane<MODE>(lane, frow, fq, fsw);
@@ -607,9 +637,6 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
       f8_read(nb, f8_b0, f8_b1, j, f8_b[j]);
     }
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-
   dma(stage_a<0>(), stage_b<0>(), 0);
   dma(stage_a<1>(), stage_b<1>(), 1);
   wait_stage<G::DMA_INSTR + G::DMA_INSTR_B>();  // stage 0 landed (own loads)
@@ -622,7 +649,6 @@ __device__ __forceinline__ void mainloop_dma(const uint8_t* __restrict__ A, cons
   } else {
     read_frags<MODE, G>(stage_a<0>(), stage_b<0>(), 0, a_row0, b_row0, fq, fsw, f0);
   }
-  const int64_t kt_padded = (kt_count + 1) / 2 * 2;
   for (int64_t kt = 0; kt < kt_padded; kt += 2) {
     if constexpr (MODE == F8) {
       stage_f8(I0{}, kt);
